@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Tree-verify throughput on one MI355X: one verify step = tree K/V append + packed tree attention.
+
+    python bench.py [--steps K] [--warmup W] [--config 4] [--cpu-requests 16]
+
+Default workload is BASELINE config 4 (the long-context, bandwidth-bound verify):
+64 requests, prefix ~ U[8k, 32k], 64-node trees of depth <= 8, Qwen3-8B attention
+geometry (32 q / 8 kv heads x 128, bf16), 256-token pages from a ~90 % full permuted
+pool, N(0, 1) operands, synthetic and seeded.  One step is what one decoder layer
+does per verify round on this hot path: store_kvcache of the 4096 tree K/V rows into
+their scratch slots, then one packed_tree_attention launch.  Inputs are resident in
+HBM before timing starts.
+
+Prints ONE JSON line.  `value` = query rows (tree tokens) verified per second.
+`roofline` is for the dominant kernel (tree attention): algorithmic bytes per launch
+(K/V of every visible position once per request and KV head + Q + O) over its mean
+duration from HIP events on the launch stream.  `cpu_baseline` times the reference's
+PyTorch CPU path (oracle/cpu_path.py) on a bounded sample of the same batch.
+Other configs (--config 1/2/3/5) are for measurement only.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+from pathlib import Path
+import statistics
+import sys
+import time
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "nano-vllm-jetspec_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "tree-verify tokens/sec + achieved HBM GB/s (% of peak) on 1 MI355X"
+WORKLOADS = {
+    1: "cfg1: 1 request, P=512, 16-node tree depth<=5 (+ append)",
+    2: "cfg2: 8 requests, P~U[256,4096], trees of {16,32,64} nodes depth<=8",
+    3: "cfg3: accepted-only commit, 36 layers, 64 requests x 32-node scratch trees, P~U[1k,8k]",
+    4: "cfg4: 64 requests, P~U[8k,32k], 64-node trees depth<=8, ~90% full permuted pool",
+    5: "cfg5: 16 x 512-row causal chunks on P~U[0,16k] + 32 x 32-node trees on P~U[2k,8k]",
+}
+
+
+def parse_args():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--config", type=int, default=4, choices=sorted(WORKLOADS))
+    parser.add_argument("--cpu-requests", type=int, default=16,
+                        help="requests of the batch timed on the CPU path (0 disables the CPU baseline)")
+    parser.add_argument("--seed", type=int, default=None)
+    return parser.parse_args()
+
+
+def traffic_bytes(config: int):
+    """HBM bytes per attention launch measured with rocprofv3 PMC counters (committed summary)."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    entry = data.get(f"cfg{config}")
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(batch, requests: int) -> dict:
+    """The reference's PyTorch CPU path on the first `requests` requests of the same batch."""
+    import torch
+
+    from oracle import cpu_path  # CPU baseline leg only
+    from jetspec_amd import PackedTreeMetadata, workloads
+
+    meta = batch.metadata
+    chosen = list(range(min(requests, meta.num_requests)))
+    block = meta.block_size
+    slots_all = meta.tree_slots.cpu()
+    pages = sorted({p for r in chosen for p in meta.block_tables_host[r]} |
+                   {int(s) // block for r in chosen for s in slots_all[meta.request_slice(r)].tolist()})
+    remap = {p: i for i, p in enumerate(pages)}
+    index = torch.tensor(pages, device=batch.k_pool.device)
+    k_pool = batch.k_pool.index_select(0, index).cpu()
+    v_pool = batch.v_pool.index_select(0, index).cpu()
+    rows = torch.cat([torch.arange(meta.request_slice(r).start, meta.request_slice(r).stop) for r in chosen])
+    q = batch.q[rows.to(batch.q.device)].cpu()
+    new_k = batch.new_k[rows.to(batch.q.device)].cpu()
+    new_v = batch.new_v[rows.to(batch.q.device)].cpu()
+    slots = [torch.tensor([remap[int(s) // block] * block + int(s) % block
+                           for s in slots_all[meta.request_slice(r)].tolist()]) for r in chosen]
+    ancestors = [torch.from_numpy(workloads.ancestor_mask(batch.parents[r])) for r in chosen]
+    sub = PackedTreeMetadata.build([meta.prefix_lengths[r] for r in chosen],
+                                   [[remap[p] for p in meta.block_tables_host[r]] for r in chosen],
+                                   slots, ancestors, block)
+    threads = torch.get_num_threads()
+
+    def step():
+        cpu_path.append(k_pool, v_pool, new_k, new_v, sub.tree_slots)
+        cpu_path.packed_attention(q, k_pool, v_pool, sub, ancestors, batch.scale)
+
+    step()  # warmup
+    samples = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        samples.append(time.perf_counter() - t0)
+    seconds = statistics.median(samples)
+    return {"value": sub.total_queries / seconds, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"requests 0..{len(chosen) - 1} of the same batch ({sub.total_queries} tree rows, "
+                      f"{sum(sub.prefix_lengths)} prefix tokens); append + bf16 SDPA over page-table-gathered K/V; "
+                      f"median of 3 after 1 warmup, samples_s={[round(s, 3) for s in samples]}"}
+
+
+def run_verify(args, torch):
+    from jetspec_amd import packed_tree_attention, read_and_clear_status, store_kvcache, workloads
+
+    builder = {1: workloads.config1, 2: workloads.config2, 4: workloads.config4, 5: workloads.config5}[args.config]
+    kwargs = {} if args.seed is None else {"seed": args.seed}
+    batch = builder("cuda", **kwargs)
+    meta = batch.metadata
+    stream = torch.cuda.current_stream()
+
+    def step(events=None):
+        if events is not None:
+            events[0].record(stream)
+        store_kvcache(batch.new_k, batch.new_v, batch.k_pool, batch.v_pool, meta.tree_slots)
+        if events is not None:
+            events[1].record(stream)
+        out = packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, batch.groups)
+        if events is not None:
+            events[2].record(stream)
+        return out
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    status = read_and_clear_status("cuda")
+    if status:
+        raise RuntimeError(f"kernel status bits {status}: an index was out of range")
+    attn_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events)
+    append_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    algo_bytes = batch.algorithmic_bytes()
+    achieved = algo_bytes / (attn_ms * 1e-3) / 1e9
+    tokens = meta.total_queries
+    result = {
+        "metric": METRIC, "value": tokens * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, seeded parent arrays, permuted page pool)",
+        "config": {"workload": WORKLOADS[args.config], "requests": meta.num_requests,
+                   "tree_rows_per_step": tokens, "prefix_tokens": sum(meta.prefix_lengths),
+                   "q_heads": 32, "kv_heads": 8, "head_dim": 128, "page": meta.block_size, "layers_per_step": 1,
+                   "pool_pages": batch.info["pages"]},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes(args.config),
+                     "kernel": "tree_attention_kernel", "kernel_ms": attn_ms, "algorithmic_bytes": algo_bytes,
+                     "algorithmic_flops": batch.algorithmic_flops(),
+                     "achieved_tflops": batch.algorithmic_flops() / (attn_ms * 1e-3) / 1e12,
+                     "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
+    }
+    if args.cpu_requests > 0 and args.config in (1, 2, 4, 5):
+        result["cpu_baseline"] = cpu_baseline(batch, args.cpu_requests)
+    return result
+
+
+def run_commit(args, torch):
+    from jetspec_amd import copy_accepted_kv, read_and_clear_status, workloads
+
+    batch = workloads.config3("cuda") if args.seed is None else workloads.config3("cuda", seed=args.seed)
+    pool, src, dst = batch.kv_pool, batch.source, batch.destination
+    for _ in range(args.warmup):
+        copy_accepted_kv(pool, src, dst, pool.shape[3])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e in events:
+        e[0].record(stream)
+        copy_accepted_kv(pool, src, dst, pool.shape[3])
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    if read_and_clear_status("cuda"):
+        raise RuntimeError("commit reported an out-of-range slot")
+    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    algo = batch.algorithmic_bytes()
+    achieved = algo / (ms * 1e-3) / 1e9
+    rows = int(src.numel())
+    return {"metric": "accepted KV rows committed/sec (36 layers) + achieved HBM GB/s", "value": rows * args.steps / elapsed,
+            "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": WORKLOADS[3], "accepted_rows": rows, "pool_pages": batch.info["pages"]},
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes(3), "kernel_ms": ms,
+                         "algorithmic_bytes": algo}}
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (--gpus {args.gpus} refused)",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        return 1
+    result = run_commit(args, torch) if args.config == 3 else run_verify(args, torch)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

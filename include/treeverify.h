@@ -1,0 +1,209 @@
+/*
+ * treeverify.h - C ABI of the MI355X (gfx950) tree-verification hot path.
+ *
+ * Three device operations replace the three Triton/PyTorch operations that the
+ * nano-vllm-jetspec speculative runner calls per verify round:
+ *
+ *   tv_store_kvcache      slot-mapped K/V append
+ *                         replaces layers/attention.py:38-45 (store_kvcache) and
+ *                         the eager tree scatter models/qwen3.py:255-258
+ *   tv_tree_attention     ragged packed tree-verify attention over a paged KV pool
+ *                         replaces speculative/jetspec/paged_backend.py:240-306
+ *                         (packed_tree_attention) and its kernels
+ *                         paged_backend.py:116-213, tree_prefix.py:303-441,
+ *                         tree_gqa.py:32-111
+ *   tv_copy_accepted_kv   accepted-only KV commit across both KV axes and all layers
+ *                         replaces speculative/jetspec/state.py:64-86
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer unless its name ends in _host.
+ *   - Strides are in ELEMENTS, never bytes.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream).
+ *   - Every entry point only enqueues work: no host synchronisation and no device
+ *     allocation.  Caller-owned workspaces are passed in explicitly.
+ *   - Return value: TV_OK (0) or a negative TV_ERR_* code; tv_last_error() gives
+ *     the message of the last failing call made by the calling thread.
+ *   - `status` (optional, may be NULL) is a device int32 that kernels OR error
+ *     bits into (TV_STATUS_*) when they meet an out-of-range page or slot.  The
+ *     offending K/V row is then neither read nor written, so a bad index can never
+ *     fault the GPU; the result for that row is unspecified.
+ */
+#ifndef TREEVERIFY_H
+#define TREEVERIFY_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TV_ABI_VERSION 1
+
+enum tv_error {
+    TV_OK = 0,
+    TV_ERR_INVALID = -1,      /* malformed arguments (shape, stride, pointer, count) */
+    TV_ERR_UNSUPPORTED = -2,  /* well-formed but outside what the kernels implement */
+    TV_ERR_LAUNCH = -3,       /* the HIP runtime refused a launch */
+    TV_ERR_CAPACITY = -4      /* a caller-provided buffer is too small */
+};
+
+enum tv_dtype { TV_BF16 = 0, TV_F16 = 1, TV_F32 = 2 };
+
+enum tv_status_bits {
+    TV_STATUS_BAD_PAGE = 1,    /* a block-table page or tree slot outside the pool */
+    TV_STATUS_BAD_SLOT = 2,    /* a store/commit slot outside the pool */
+    TV_STATUS_BAD_REQUEST = 4  /* metadata row that names a nonexistent request */
+};
+
+/* ABI version of the loaded library (TV_ABI_VERSION at build time). */
+int tv_abi_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* tv_last_error(void);
+
+/* sizeof(tv_tree_attention_args) as compiled into the library, so bindings can
+ * verify their struct layout before the first call. */
+int64_t tv_sizeof_tree_attention_args(void);
+
+/* ------------------------------------------------------------------------- */
+/* store_kvcache  (layers/attention.py:15-45)                                 */
+/* ------------------------------------------------------------------------- */
+/*
+ * For each row i < num_rows with slot = slot_mapping[i] != -1, copy row_elems
+ * contiguous elements of key[i] and value[i] to k_cache/v_cache at element
+ * offset slot * row_elems (the reference's `slot * D` addressing, which assumes a
+ * cache whose slot rows are dense: stride(1) == row_elems).  Bit-exact copy.
+ *   key/value row i starts at element i * key_row_stride / i * value_row_stride.
+ *   slot_mapping is int32 (slot_is_int64 == 0) or int64.
+ *   num_cache_slots bounds the slot; slots outside [0, num_cache_slots) other than
+ *   -1 are skipped and reported through `status`.
+ */
+int tv_store_kvcache(const void* key, int64_t key_row_stride,
+                     const void* value, int64_t value_row_stride,
+                     void* k_cache, void* v_cache, int64_t num_cache_slots,
+                     const void* slot_mapping, int32_t slot_is_int64,
+                     int64_t num_rows, int64_t row_elems, int32_t elem_bytes,
+                     int32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* copy_accepted_kv  (speculative/jetspec/state.py:64-86)                     */
+/* ------------------------------------------------------------------------- */
+/*
+ * kv_pool has shape [2, L, N, B, H, D] with the given element strides; a slot row
+ * (H*D elements) must be dense: stride[5] == 1 and stride[4] == D.
+ * For every kv in {0,1}, layer l < L and i < num_slots:
+ *     pool[kv, l, dst[i] / B, dst[i] % B] = pool[kv, l, src[i] / B, src[i] % B]
+ * with the reference's gather-then-scatter semantics: if any destination slot is
+ * also a source slot, all sources are read before any destination is written
+ * (through `workspace`), otherwise the rows are copied directly.
+ * workspace must hold tv_copy_accepted_kv_workspace_bytes(...) bytes.
+ * On success *payload_bytes (host, may be NULL) receives 2*L*num_slots*H*D*elem,
+ * the reference's return value.
+ */
+int64_t tv_copy_accepted_kv_workspace_bytes(int64_t num_slots, int64_t num_layers,
+                                            int64_t row_elems, int32_t elem_bytes);
+
+int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6],
+                        const int64_t pool_stride[6], int32_t elem_bytes,
+                        const int64_t* source_slots, const int64_t* destination_slots,
+                        int64_t num_slots, void* workspace, int64_t workspace_bytes,
+                        int64_t* payload_bytes_host, int32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* packed tree attention  (speculative/jetspec/paged_backend.py:240-306)      */
+/* ------------------------------------------------------------------------- */
+/*
+ * Work plan.  Splits the ragged batch into work items (request, KV-head group,
+ * node block, prefix key range) ordered longest first, and merge groups for
+ * requests whose prefix is split.  Pure host computation on the metadata's host
+ * copies (PackedTreeMetadata.prefix_lengths / node_counts_host).
+ * Call once with NULL outputs to learn the sizes (written to *info), then again
+ * with buffers of at least info->num_items * 8 and info->num_groups * 8 int32.
+ *   num_compute_units: CUs of the target device (256 on MI355X).
+ *   chunk_keys: 0 = automatic; > 0 forces every prefix chunk to that many keys
+ *               (a multiple of 32), which makes per-request results independent
+ *               of the rest of the batch.
+ */
+typedef struct tv_attention_plan_info {
+    int32_t num_items;
+    int32_t num_groups;
+    int32_t num_partial_slots;
+    int32_t ancestor_words_per_row;  /* ceil(max node count / 64) */
+    int64_t workspace_bytes;         /* device workspace tv_tree_attention needs */
+} tv_attention_plan_info;
+
+int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
+                           int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                           int32_t num_compute_units, int32_t chunk_keys,
+                           int32_t* items_host, int32_t* groups_host,
+                           tv_attention_plan_info* info);
+
+/*
+ * Packs the request-local additive ancestor bias of PackedTreeMetadata
+ * (qq_bias f32, 0 = visible / -inf = hidden, row-major [local_q * T + node] at
+ * qq_bias_offsets[r]; packed_metadata.py:93-100) into one bit per (row, node):
+ * words[q * words_per_row + w] bit b is set iff node m = 64w + b satisfies
+ * m < T, m <= local_q and qq_bias[...] == 0.
+ */
+int tv_pack_ancestor_words(const float* qq_bias, const int64_t* qq_bias_offsets,
+                           const int32_t* query_to_request, const int32_t* query_local_row,
+                           const int32_t* node_counts, int32_t total_queries,
+                           int32_t num_requests, int32_t words_per_row,
+                           uint64_t* words, int32_t* status, void* stream);
+
+typedef struct tv_tree_attention_args {
+    /* q [Q, Hq, D]; head dim contiguous */
+    const void* q;
+    int64_t q_stride_row, q_stride_head;
+    /* k/v pools [N, B, Hkv, D]; stride[3] must be 1 */
+    const void* k_pool;
+    const void* v_pool;
+    int64_t k_stride[4];
+    int64_t v_stride[4];
+    int64_t num_blocks;
+    int32_t in_dtype;                    /* TV_BF16 or TV_F16 */
+    /* out [Q, Hq, D]; head dim contiguous */
+    void* out;
+    int64_t out_stride_row, out_stride_head;
+    int32_t out_dtype;                   /* in_dtype or TV_F32 */
+    /* PackedTreeMetadata device buffers (packed_metadata.py:17-26) */
+    const int32_t* cu_seqlens_q;         /* [R+1] */
+    const int32_t* prefix_lens;          /* [R] */
+    const int32_t* node_counts;          /* [R] */
+    const int32_t* block_tables;         /* [R, table_stride], pad -1 */
+    int64_t block_table_stride;
+    const int64_t* tree_slots;           /* [Q] */
+    /* derived per metadata: tv_pack_ancestor_words */
+    const uint64_t* ancestor_words;
+    int32_t ancestor_words_per_row;
+    /* geometry */
+    int32_t num_requests, total_queries, num_q_heads, num_kv_heads, head_dim, block_size;
+    float scale;
+    /* plan: tv_tree_attention_plan, copied to the device */
+    const int32_t* items;
+    int32_t num_items;
+    const int32_t* groups;
+    int32_t num_groups;
+    int32_t num_partial_slots;
+    void* workspace;
+    int64_t workspace_bytes;
+    int32_t* status;                     /* optional */
+} tv_tree_attention_args;
+
+/*
+ * out[q, h, :] = softmax_k(scale * q[q,h,:] . K[k, h/G, :]) V[k, h/G, :] over the
+ * keys visible to packed row q of request r: every committed prefix position
+ * < prefix_lens[r] (addressed through block_tables), plus every tree node m of r
+ * whose ancestor bit is set (addressed through tree_slots).  bf16/f16 operands,
+ * fp32 accumulation and online softmax, probabilities rounded to the operand
+ * type for the P.V product (tree_gqa.py:102-105).
+ * Implemented geometry: head_dim 128, num_q_heads == 4 * num_kv_heads,
+ * block_size % 32 == 0.
+ */
+int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREEVERIFY_H */

@@ -1,0 +1,339 @@
+// Slot-mapped KV append and accepted-only KV commit for gfx950.
+//
+// Both operations are pure byte movement of 2 KiB slot rows (8 KV heads x 128 dims
+// x bf16 at the served geometry), so the kernels are written for HBM efficiency:
+// 16-byte vector loads and stores, every load of a row issued before its stores,
+// and no arithmetic beyond address generation.  Bit-exactness is by construction.
+#include <stdint.h>
+
+#include "tv_internal.h"
+
+namespace tv {
+namespace {
+
+// ------------------------------------------------------------------ store_kvcache
+// layers/attention.py:15-35: program idx copies key/value row idx to cache row
+// slot_mapping[idx] unless the slot is -1.  Here one workgroup handles one row
+// per iteration; its threads cover the row in `Unit`-byte pieces.
+template <typename Unit>
+__global__ void __launch_bounds__(256)
+store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
+                     const char* __restrict__ value, int64_t value_stride_b,
+                     char* __restrict__ k_cache, char* __restrict__ v_cache,
+                     int64_t num_slots, const void* __restrict__ slots, int slot_is_int64,
+                     int64_t num_rows, int32_t units_per_row, int32_t* status) {
+    const int64_t row_bytes = static_cast<int64_t>(units_per_row) * sizeof(Unit);
+    for (int64_t row = blockIdx.x; row < num_rows; row += gridDim.x) {
+        const int64_t slot = slot_is_int64 ? static_cast<const int64_t*>(slots)[row]
+                                           : static_cast<int64_t>(static_cast<const int32_t*>(slots)[row]);
+        if (slot == -1) continue;
+        if (slot < 0 || slot >= num_slots) {
+            if (threadIdx.x == 0) set_status(status, TV_STATUS_BAD_SLOT);
+            continue;
+        }
+        const char* ksrc = key + row * key_stride_b;
+        const char* vsrc = value + row * value_stride_b;
+        char* kdst = k_cache + slot * row_bytes;
+        char* vdst = v_cache + slot * row_bytes;
+        for (int32_t u = threadIdx.x; u < units_per_row; u += blockDim.x) {
+            const Unit kv = reinterpret_cast<const Unit*>(ksrc)[u];
+            const Unit vv = reinterpret_cast<const Unit*>(vsrc)[u];
+            reinterpret_cast<Unit*>(kdst)[u] = kv;
+            reinterpret_cast<Unit*>(vdst)[u] = vv;
+        }
+    }
+}
+
+// --------------------------------------------------------------- copy_accepted_kv
+// state.py:80-85 gathers pool[:, :, src] into a temporary and then scatters it to
+// pool[:, :, dst], so an overlap between the two slot sets is well defined.  The
+// served callers never overlap (scratch arena pages vs owned/pending pages,
+// state.py:687-688), so the fast path copies rows directly and only an actual
+// overlap takes the staged path:
+//   1. commit_check:   per 256 destinations, OR of {overlap with any source,
+//                      out-of-range slot}; one flag word per workgroup, always
+//                      written, so the workspace needs no clearing.
+//   2. commit_copy:    no flag -> direct copy; overlap -> gather into workspace.
+//   3. commit_scatter: overlap -> scatter workspace to destinations; else exits.
+
+constexpr int kCheckThreads = 256;
+constexpr int kSrcTile = 1024;
+constexpr int kFlagOverlap = 1;
+constexpr int kFlagInvalid = 2;
+
+__global__ void __launch_bounds__(kCheckThreads)
+commit_check_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
+                    int64_t n, int64_t pool_slots, int32_t* __restrict__ flags,
+                    int32_t* status) {
+    __shared__ int64_t tile[kSrcTile];
+    __shared__ int32_t block_flag;
+    if (threadIdx.x == 0) block_flag = 0;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kCheckThreads + threadIdx.x;
+    int32_t flag = 0;
+    int64_t d = -1;
+    if (j < n) {
+        d = dst[j];
+        const int64_t s = src[j];
+        if (d < 0 || d >= pool_slots || s < 0 || s >= pool_slots) flag |= kFlagInvalid;
+    }
+    for (int64_t base = 0; base < n; base += kSrcTile) {
+        const int64_t count = (n - base < kSrcTile) ? (n - base) : kSrcTile;
+        __syncthreads();
+        for (int64_t k = threadIdx.x; k < count; k += kCheckThreads) tile[k] = src[base + k];
+        __syncthreads();
+        if (j < n) {
+            for (int64_t k = 0; k < count; ++k) {
+                if (tile[k] == d) flag |= kFlagOverlap;
+            }
+        }
+    }
+    if (flag) atomicOr(&block_flag, flag);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        flags[blockIdx.x] = block_flag;
+        if (block_flag & kFlagInvalid) set_status(status, TV_STATUS_BAD_SLOT);
+    }
+}
+
+__device__ __forceinline__ int32_t read_flags(const int32_t* flags, int32_t num_flags) {
+    __shared__ int32_t combined;
+    if (threadIdx.x == 0) combined = 0;
+    __syncthreads();
+    int32_t f = 0;
+    for (int32_t k = threadIdx.x; k < num_flags; k += blockDim.x) f |= flags[k];
+    if (f) atomicOr(&combined, f);
+    __syncthreads();
+    return combined;
+}
+
+struct PoolGeom {
+    char* base;
+    int64_t s_kv, s_layer, s_block, s_off;  // bytes
+    int64_t layers, block_size, n;
+    int32_t units_per_row;
+};
+
+__device__ __forceinline__ char* slot_row(const PoolGeom& g, int64_t kv, int64_t layer, int64_t slot) {
+    const int64_t block = slot / g.block_size;
+    const int64_t off = slot - block * g.block_size;
+    return g.base + kv * g.s_kv + layer * g.s_layer + block * g.s_block + off * g.s_off;
+}
+
+// mode 0: direct src -> dst (only when no flag is set)
+// mode 1: gather src -> workspace (only when the overlap flag alone is set)
+// mode 2: scatter workspace -> dst (only when the overlap flag alone is set)
+template <typename Unit, int kMode>
+__global__ void __launch_bounds__(256)
+commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
+                   const int32_t* __restrict__ flags, int32_t num_flags,
+                   Unit* __restrict__ staging) {
+    const int32_t f = read_flags(flags, num_flags);
+    if (kMode == 0 && f != 0) return;
+    if (kMode != 0 && f != kFlagOverlap) return;
+    const int64_t rows = 2 * g.layers * g.n;
+    const int32_t upr = g.units_per_row;
+    // Each iteration a workgroup moves `rows_per_iter` rows; a thread owns one
+    // unit of one row, so all loads of the iteration are in flight together.
+    const int32_t rows_per_iter = upr >= 256 ? 1 : 256 / upr;
+    const int32_t sub = upr >= 256 ? 0 : threadIdx.x / upr;
+    const int32_t lane_unit = upr >= 256 ? threadIdx.x : threadIdx.x % upr;
+    if (sub >= rows_per_iter) return;
+    for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * rows_per_iter; row0 < rows;
+         row0 += static_cast<int64_t>(gridDim.x) * rows_per_iter) {
+        const int64_t row = row0 + sub;
+        if (row >= rows) break;
+        const int64_t i = row % g.n;
+        const int64_t kl = row / g.n;
+        const int64_t layer = kl % g.layers;
+        const int64_t kv = kl / g.layers;
+        if (kMode == 0) {
+            const Unit* s = reinterpret_cast<const Unit*>(slot_row(g, kv, layer, src[i]));
+            Unit* d = reinterpret_cast<Unit*>(slot_row(g, kv, layer, dst[i]));
+            for (int32_t u = lane_unit; u < upr; u += 256) d[u] = s[u];
+        } else if (kMode == 1) {
+            const Unit* s = reinterpret_cast<const Unit*>(slot_row(g, kv, layer, src[i]));
+            Unit* d = staging + row * upr;
+            for (int32_t u = lane_unit; u < upr; u += 256) d[u] = s[u];
+        } else {
+            const Unit* s = staging + row * upr;
+            Unit* d = reinterpret_cast<Unit*>(slot_row(g, kv, layer, dst[i]));
+            for (int32_t u = lane_unit; u < upr; u += 256) d[u] = s[u];
+        }
+    }
+}
+
+template <typename Unit>
+int launch_commit(const PoolGeom& g, const int64_t* src, const int64_t* dst, int32_t* flags,
+                  int32_t num_flags, void* staging, hipStream_t stream) {
+    const int64_t rows = 2 * g.layers * g.n;
+    const int32_t rows_per_iter = g.units_per_row >= 256 ? 1 : 256 / g.units_per_row;
+    int64_t blocks = (rows + rows_per_iter - 1) / rows_per_iter;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks < 1) blocks = 1;
+    Unit* st = static_cast<Unit*>(staging);
+    hipLaunchKernelGGL((commit_move_kernel<Unit, 0>), dim3(blocks), dim3(256), 0, stream, g, src, dst,
+                       flags, num_flags, st);
+    hipLaunchKernelGGL((commit_move_kernel<Unit, 1>), dim3(blocks), dim3(256), 0, stream, g, src, dst,
+                       flags, num_flags, st);
+    hipLaunchKernelGGL((commit_move_kernel<Unit, 2>), dim3(blocks), dim3(256), 0, stream, g, src, dst,
+                       flags, num_flags, st);
+    return check_launch("copy_accepted_kv");
+}
+
+int unit_for(int64_t alignment_bytes) {
+    if (alignment_bytes % 16 == 0) return 16;
+    if (alignment_bytes % 8 == 0) return 8;
+    if (alignment_bytes % 4 == 0) return 4;
+    if (alignment_bytes % 2 == 0) return 2;
+    return 1;
+}
+
+int64_t gcd64(int64_t a, int64_t b) {
+    a = a < 0 ? -a : a;
+    b = b < 0 ? -b : b;
+    while (b) {
+        const int64_t t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
+}
+
+int64_t num_flag_words(int64_t n) { return (n + kCheckThreads - 1) / kCheckThreads; }
+
+}  // namespace
+}  // namespace tv
+
+using namespace tv;
+
+extern "C" int tv_store_kvcache(const void* key, int64_t key_row_stride, const void* value,
+                                int64_t value_row_stride, void* k_cache, void* v_cache,
+                                int64_t num_cache_slots, const void* slot_mapping,
+                                int32_t slot_is_int64, int64_t num_rows, int64_t row_elems,
+                                int32_t elem_bytes, int32_t* status, void* stream) {
+    clear_error();
+    if (num_rows < 0 || row_elems <= 0 || num_cache_slots < 0) {
+        return fail(TV_ERR_INVALID, "store_kvcache: invalid sizes rows=%lld row_elems=%lld",
+                    (long long)num_rows, (long long)row_elems);
+    }
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) {
+        return fail(TV_ERR_INVALID, "store_kvcache: element size %d", elem_bytes);
+    }
+    if (num_rows == 0) return TV_OK;
+    if (!key || !value || !k_cache || !v_cache || !slot_mapping) {
+        return fail(TV_ERR_INVALID, "store_kvcache: null pointer");
+    }
+    const int64_t row_bytes = row_elems * elem_bytes;
+    int64_t align = gcd64(row_bytes, gcd64(key_row_stride * elem_bytes, value_row_stride * elem_bytes));
+    align = gcd64(align, static_cast<int64_t>(reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value) |
+                                              reinterpret_cast<uintptr_t>(k_cache) |
+                                              reinterpret_cast<uintptr_t>(v_cache)) | 16);
+    if (align == 0) align = 16;
+    const int unit = unit_for(align);
+    const int32_t units = static_cast<int32_t>(row_bytes / unit);
+    int threads = 64;
+    while (threads < units && threads < 256) threads *= 2;
+    int64_t blocks = num_rows < 65536 ? num_rows : 65536;
+    hipStream_t s = as_stream(stream);
+    const char* k = static_cast<const char*>(key);
+    const char* v = static_cast<const char*>(value);
+    char* kc = static_cast<char*>(k_cache);
+    char* vc = static_cast<char*>(v_cache);
+    const int64_t ks = key_row_stride * elem_bytes, vs = value_row_stride * elem_bytes;
+    switch (unit) {
+        case 16:
+            hipLaunchKernelGGL(store_kvcache_kernel<u32x4>, dim3(blocks), dim3(threads), 0, s, k, ks, v, vs,
+                               kc, vc, num_cache_slots, slot_mapping, slot_is_int64, num_rows, units, status);
+            break;
+        case 8:
+            hipLaunchKernelGGL(store_kvcache_kernel<u32x2>, dim3(blocks), dim3(threads), 0, s, k, ks, v, vs,
+                               kc, vc, num_cache_slots, slot_mapping, slot_is_int64, num_rows, units, status);
+            break;
+        case 4:
+            hipLaunchKernelGGL(store_kvcache_kernel<uint32_t>, dim3(blocks), dim3(threads), 0, s, k, ks, v, vs,
+                               kc, vc, num_cache_slots, slot_mapping, slot_is_int64, num_rows, units, status);
+            break;
+        case 2:
+            hipLaunchKernelGGL(store_kvcache_kernel<uint16_t>, dim3(blocks), dim3(threads), 0, s, k, ks, v, vs,
+                               kc, vc, num_cache_slots, slot_mapping, slot_is_int64, num_rows, units, status);
+            break;
+        default:
+            hipLaunchKernelGGL(store_kvcache_kernel<uint8_t>, dim3(blocks), dim3(threads), 0, s, k, ks, v, vs,
+                               kc, vc, num_cache_slots, slot_mapping, slot_is_int64, num_rows, units, status);
+            break;
+    }
+    return check_launch("store_kvcache");
+}
+
+extern "C" int64_t tv_copy_accepted_kv_workspace_bytes(int64_t num_slots, int64_t num_layers,
+                                                       int64_t row_elems, int32_t elem_bytes) {
+    if (num_slots <= 0 || num_layers <= 0 || row_elems <= 0 || elem_bytes <= 0) return 0;
+    const int64_t flag_bytes = ((num_flag_words(num_slots) * 4 + 255) / 256) * 256;
+    return flag_bytes + 2 * num_layers * num_slots * row_elems * elem_bytes;
+}
+
+extern "C" int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6], const int64_t pool_stride[6],
+                                   int32_t elem_bytes, const int64_t* source_slots,
+                                   const int64_t* destination_slots, int64_t num_slots, void* workspace,
+                                   int64_t workspace_bytes, int64_t* payload_bytes_host, int32_t* status,
+                                   void* stream) {
+    clear_error();
+    if (!pool_shape || !pool_stride) return fail(TV_ERR_INVALID, "copy_accepted_kv: null geometry");
+    if (pool_shape[0] != 2) return fail(TV_ERR_INVALID, "copy_accepted_kv: pool axis 0 must be 2 (K, V)");
+    for (int d = 0; d < 6; ++d) {
+        if (pool_shape[d] <= 0) return fail(TV_ERR_INVALID, "copy_accepted_kv: empty pool axis %d", d);
+        if (pool_stride[d] < 0) return fail(TV_ERR_INVALID, "copy_accepted_kv: negative stride %d", d);
+    }
+    if (pool_stride[5] != 1 || pool_stride[4] != pool_shape[5]) {
+        return fail(TV_ERR_UNSUPPORTED, "copy_accepted_kv: a slot row [heads, dim] must be dense");
+    }
+    if (num_slots < 0) return fail(TV_ERR_INVALID, "copy_accepted_kv: negative slot count");
+    const int64_t layers = pool_shape[1];
+    const int64_t row_elems = pool_shape[4] * pool_shape[5];
+    const int64_t payload = 2 * layers * num_slots * row_elems * elem_bytes;
+    if (num_slots == 0) {
+        if (payload_bytes_host) *payload_bytes_host = 0;
+        return TV_OK;
+    }
+    if (!kv_pool || !source_slots || !destination_slots || !workspace) {
+        return fail(TV_ERR_INVALID, "copy_accepted_kv: null pointer");
+    }
+    const int64_t need = tv_copy_accepted_kv_workspace_bytes(num_slots, layers, row_elems, elem_bytes);
+    if (workspace_bytes < need) {
+        return fail(TV_ERR_CAPACITY, "copy_accepted_kv: workspace %lld < %lld bytes", (long long)workspace_bytes,
+                    (long long)need);
+    }
+    PoolGeom g;
+    g.base = static_cast<char*>(kv_pool);
+    g.s_kv = pool_stride[0] * elem_bytes;
+    g.s_layer = pool_stride[1] * elem_bytes;
+    g.s_block = pool_stride[2] * elem_bytes;
+    g.s_off = pool_stride[3] * elem_bytes;
+    g.layers = layers;
+    g.block_size = pool_shape[3];
+    g.n = num_slots;
+    const int64_t row_bytes = row_elems * elem_bytes;
+    int64_t align = gcd64(row_bytes, gcd64(g.s_kv, gcd64(g.s_layer, gcd64(g.s_block, g.s_off))));
+    align = gcd64(align, static_cast<int64_t>(reinterpret_cast<uintptr_t>(kv_pool) | 16));
+    const int unit = unit_for(align);
+    g.units_per_row = static_cast<int32_t>(row_bytes / unit);
+    const int64_t pool_slots = pool_shape[2] * pool_shape[3];
+    const int32_t nflags = static_cast<int32_t>(num_flag_words(num_slots));
+    int32_t* flags = static_cast<int32_t*>(workspace);
+    const int64_t flag_bytes = ((static_cast<int64_t>(nflags) * 4 + 255) / 256) * 256;
+    void* staging = static_cast<char*>(workspace) + flag_bytes;
+    hipStream_t s = as_stream(stream);
+    hipLaunchKernelGGL(commit_check_kernel, dim3(nflags), dim3(kCheckThreads), 0, s, source_slots,
+                       destination_slots, num_slots, pool_slots, flags, status);
+    int rc;
+    switch (unit) {
+        case 16: rc = launch_commit<u32x4>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
+        case 8: rc = launch_commit<u32x2>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
+        case 4: rc = launch_commit<uint32_t>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
+        case 2: rc = launch_commit<uint16_t>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
+        default: rc = launch_commit<uint8_t>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
+    }
+    if (rc != TV_OK) return rc;
+    if (payload_bytes_host) *payload_bytes_host = payload;
+    return TV_OK;
+}

@@ -1,0 +1,162 @@
+// Host-side work planner for the packed tree-verify attention kernel.
+//
+// The reference launches one program per (packed query, query head)
+// (paged_backend.py:290) or per (4-node block, KV head) (tree_gqa.py:130), and every
+// program walks its request's whole prefix.  On MI355X the kernel instead gives a
+// 512-thread workgroup 256 score rows that share one K/V stream:
+//   HPW (KV heads per workgroup) = 4 / 2 / 1 for trees of <=16 / <=32 / >32 nodes,
+//   NPW (nodes per workgroup)    = 64 / HPW,
+// so a KV tile staged in LDS is reused by every (node, query head) row of its group.
+// Long prefixes are cut into chunks (split-K) only as far as needed to give every
+// compute unit work; items are ordered longest first so the hardware dispatcher's
+// greedy assignment balances ragged contexts (an LPT schedule).
+#include <stdint.h>
+
+#include <algorithm>
+#include <vector>
+
+#include "tv_internal.h"
+
+namespace tv {
+namespace {
+
+constexpr int kItemInts = 8;
+constexpr int kRowsPerItem = 256;   // score rows of one workgroup
+constexpr int kHeadDim = 128;
+constexpr int kMinChunkKeys = 256;  // shortest prefix chunk worth a partial result
+
+struct Item {
+    int32_t r, h0, n0, kbeg, kend, flags, slot, hpw;
+    int64_t cost;
+    int32_t hg, chunk, nb;
+};
+
+int heads_per_group(int32_t nodes, int32_t kv_heads) {
+    int h = nodes <= 16 ? 4 : (nodes <= 32 ? 2 : 1);
+    while (h > 1 && h > kv_heads) h >>= 1;
+    return h;
+}
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+}  // namespace
+}  // namespace tv
+
+using namespace tv;
+
+extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
+                                      int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                      int32_t num_compute_units, int32_t chunk_keys, int32_t* items_host,
+                                      int32_t* groups_host, tv_attention_plan_info* info) {
+    clear_error();
+    if (!info || !prefix_lens_host || !node_counts_host) return fail(TV_ERR_INVALID, "plan: null argument");
+    if (num_requests < 1) return fail(TV_ERR_INVALID, "plan: at least one request is required");
+    if (num_kv_heads < 1) return fail(TV_ERR_INVALID, "plan: num_kv_heads must be positive");
+    if (block_size < 32 || block_size % 32) {
+        return fail(TV_ERR_UNSUPPORTED, "plan: block_size %d is not a positive multiple of 32", block_size);
+    }
+    if (num_compute_units < 1) return fail(TV_ERR_INVALID, "plan: num_compute_units must be positive");
+    if (chunk_keys < 0 || chunk_keys % 32) {
+        return fail(TV_ERR_INVALID, "plan: chunk_keys %d must be a non-negative multiple of 32", chunk_keys);
+    }
+    int32_t max_nodes = 1;
+    int64_t total_cost = 0;
+    for (int32_t r = 0; r < num_requests; ++r) {
+        const int32_t p = prefix_lens_host[r], t = node_counts_host[r];
+        if (p < 0) return fail(TV_ERR_INVALID, "plan: negative prefix length for request %d", r);
+        if (t < 1) return fail(TV_ERR_INVALID, "plan: request %d has no tree nodes", r);
+        max_nodes = std::max(max_nodes, t);
+        const int hpw = heads_per_group(t, num_kv_heads);
+        const int npw = 64 / hpw;
+        const int64_t groups = (num_kv_heads + hpw - 1) / hpw;
+        const int64_t blocks = (t + npw - 1) / npw;
+        total_cost += groups * blocks * hpw * (static_cast<int64_t>(p) + t);
+    }
+    const int64_t target = std::max<int64_t>(kMinChunkKeys, total_cost / num_compute_units);
+
+    std::vector<Item> items;
+    int32_t num_slots = 0, num_groups = 0;
+    for (int32_t r = 0; r < num_requests; ++r) {
+        const int32_t p = prefix_lens_host[r], t = node_counts_host[r];
+        const int hpw = heads_per_group(t, num_kv_heads);
+        const int npw = 64 / hpw;
+        const int32_t groups = (num_kv_heads + hpw - 1) / hpw;
+        const int32_t blocks = (t + npw - 1) / npw;
+        int64_t chunk;
+        if (chunk_keys > 0) {
+            chunk = chunk_keys;
+        } else {
+            chunk = round_up(std::max<int64_t>(kMinChunkKeys, target / hpw), 32);
+            const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
+            chunk = round_up((p + nchunks - 1) / std::max<int64_t>(nchunks, 1), 32);
+            if (chunk < 32) chunk = 32;
+        }
+        const int32_t nchunks = p > 0 ? static_cast<int32_t>((p + chunk - 1) / chunk) : 1;
+        for (int32_t hg = 0; hg < groups; ++hg) {
+            for (int32_t nb = 0; nb < blocks; ++nb) {
+                const int32_t first_slot = nchunks > 1 ? num_slots : -1;
+                for (int32_t c = 0; c < nchunks; ++c) {
+                    Item it;
+                    it.r = r;
+                    it.h0 = hg * hpw;
+                    it.n0 = nb * npw;
+                    it.kbeg = static_cast<int32_t>(std::min<int64_t>(p, c * chunk));
+                    it.kend = static_cast<int32_t>(std::min<int64_t>(p, (c + 1) * chunk));
+                    it.flags = (c == nchunks - 1) ? 1 : 0;
+                    it.slot = nchunks > 1 ? first_slot + c : -1;
+                    it.hpw = hpw;
+                    // Node blocks of one (request, head group, chunk) share their K/V
+                    // stream, so they get equal cost and stay adjacent after sorting.
+                    it.cost = static_cast<int64_t>(hpw) * ((it.kend - it.kbeg) + (it.flags ? t : 0));
+                    it.hg = hg;
+                    it.chunk = c;
+                    it.nb = nb;
+                    items.push_back(it);
+                }
+                if (nchunks > 1) {
+                    if (groups_host) {
+                        int32_t* gr = groups_host + kItemInts * num_groups;
+                        gr[0] = r;
+                        gr[1] = hg * hpw;
+                        gr[2] = nb * npw;
+                        gr[3] = hpw;
+                        gr[4] = first_slot;
+                        gr[5] = nchunks;
+                        gr[6] = 0;
+                        gr[7] = 0;
+                    }
+                    num_slots += nchunks;
+                    ++num_groups;
+                }
+            }
+        }
+    }
+    std::stable_sort(items.begin(), items.end(), [](const Item& a, const Item& b) {
+        if (a.cost != b.cost) return a.cost > b.cost;
+        if (a.r != b.r) return a.r < b.r;
+        if (a.hg != b.hg) return a.hg < b.hg;
+        if (a.chunk != b.chunk) return a.chunk < b.chunk;
+        return a.nb < b.nb;
+    });
+    if (items_host) {
+        for (size_t i = 0; i < items.size(); ++i) {
+            int32_t* o = items_host + kItemInts * i;
+            o[0] = items[i].r;
+            o[1] = items[i].h0;
+            o[2] = items[i].n0;
+            o[3] = items[i].kbeg;
+            o[4] = items[i].kend;
+            o[5] = items[i].flags;
+            o[6] = items[i].slot;
+            o[7] = items[i].hpw;
+        }
+    }
+    info->num_items = static_cast<int32_t>(items.size());
+    info->num_groups = num_groups;
+    info->num_partial_slots = num_slots;
+    info->ancestor_words_per_row = (max_nodes + 63) / 64;
+    const int64_t o_bytes = static_cast<int64_t>(num_slots) * kRowsPerItem * kHeadDim * 4;
+    const int64_t ml_bytes = static_cast<int64_t>(num_slots) * kRowsPerItem * 8;
+    info->workspace_bytes = num_slots ? round_up(o_bytes, 256) + round_up(ml_bytes, 256) : 0;
+    return TV_OK;
+}

@@ -1,0 +1,43 @@
+"""MI355X-native tree-verification hot path of nano-vllm-jetspec.
+
+Drop-in operators (same names, arguments and errors as the reference):
+  packed_tree_attention   speculative/jetspec/paged_backend.py:240-306
+  store_kvcache           layers/attention.py:38-45
+  copy_accepted_kv        speculative/jetspec/state.py:64-86
+  PackedTreeMetadata      speculative/jetspec/packed_metadata.py:16-237
+  accept_batch            speculative/jetspec/serving_ops.py:55-90
+Each device operator is a hand-written gfx950 HIP kernel in libtreeverify.so.
+"""
+from .packed_metadata import PackedTreeMetadata
+from .paged_backend import (
+    packed_tree_attention,
+    packed_tree_attention_gqa,
+    packed_tree_attention_prefix_prevalidated,
+    packed_tree_attention_prefix_split_exact,
+    packed_tree_attention_reference,
+    packed_tree_attention_register_tuned,
+    paged_tree_attention,
+)
+from .attention import store_kvcache
+from .state import copy_accepted_kv, _slots_for_blocks
+from .serving_ops import accept_batch, accept_walk, build_child_maps
+from ._device import read_and_clear_status
+from ._lib import library
+
+__all__ = [
+    "PackedTreeMetadata",
+    "packed_tree_attention",
+    "packed_tree_attention_gqa",
+    "packed_tree_attention_prefix_prevalidated",
+    "packed_tree_attention_prefix_split_exact",
+    "packed_tree_attention_reference",
+    "packed_tree_attention_register_tuned",
+    "paged_tree_attention",
+    "store_kvcache",
+    "copy_accepted_kv",
+    "accept_batch",
+    "accept_walk",
+    "build_child_maps",
+    "read_and_clear_status",
+    "library",
+]

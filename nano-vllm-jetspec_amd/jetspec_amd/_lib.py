@@ -1,0 +1,160 @@
+"""ctypes binding of libtreeverify.so (the C ABI declared in include/treeverify.h).
+
+The shared library is built in-tree by ``nano-vllm-jetspec_amd/build.py``.  There
+is no fallback: if the library is missing or does not match this binding, every
+device entry point raises ``RuntimeError`` naming the problem.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_void_p
+from pathlib import Path
+import threading
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libtreeverify.so"
+ABI_VERSION = 1
+
+TV_OK = 0
+TV_ERR_INVALID = -1
+TV_ERR_UNSUPPORTED = -2
+TV_ERR_LAUNCH = -3
+TV_ERR_CAPACITY = -4
+
+TV_BF16 = 0
+TV_F16 = 1
+TV_F32 = 2
+
+TV_STATUS_BAD_PAGE = 1
+TV_STATUS_BAD_SLOT = 2
+TV_STATUS_BAD_REQUEST = 4
+
+# Every extern "C" symbol of include/treeverify.h.
+EXPORTED_SYMBOLS = (
+    "tv_abi_version",
+    "tv_last_error",
+    "tv_sizeof_tree_attention_args",
+    "tv_store_kvcache",
+    "tv_copy_accepted_kv_workspace_bytes",
+    "tv_copy_accepted_kv",
+    "tv_tree_attention_plan",
+    "tv_pack_ancestor_words",
+    "tv_tree_attention",
+)
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("num_items", c_int32),
+        ("num_groups", c_int32),
+        ("num_partial_slots", c_int32),
+        ("ancestor_words_per_row", c_int32),
+        ("workspace_bytes", c_int64),
+    ]
+
+
+class TreeAttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_void_p),
+        ("q_stride_row", c_int64),
+        ("q_stride_head", c_int64),
+        ("k_pool", c_void_p),
+        ("v_pool", c_void_p),
+        ("k_stride", c_int64 * 4),
+        ("v_stride", c_int64 * 4),
+        ("num_blocks", c_int64),
+        ("in_dtype", c_int32),
+        ("out", c_void_p),
+        ("out_stride_row", c_int64),
+        ("out_stride_head", c_int64),
+        ("out_dtype", c_int32),
+        ("cu_seqlens_q", c_void_p),
+        ("prefix_lens", c_void_p),
+        ("node_counts", c_void_p),
+        ("block_tables", c_void_p),
+        ("block_table_stride", c_int64),
+        ("tree_slots", c_void_p),
+        ("ancestor_words", c_void_p),
+        ("ancestor_words_per_row", c_int32),
+        ("num_requests", c_int32),
+        ("total_queries", c_int32),
+        ("num_q_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("block_size", c_int32),
+        ("scale", c_float),
+        ("items", c_void_p),
+        ("num_items", c_int32),
+        ("groups", c_void_p),
+        ("num_groups", c_int32),
+        ("num_partial_slots", c_int32),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_int64),
+        ("status", c_void_p),
+    ]
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.tv_abi_version.restype = c_int32
+    lib.tv_abi_version.argtypes = []
+    lib.tv_last_error.restype = c_char_p
+    lib.tv_last_error.argtypes = []
+    lib.tv_sizeof_tree_attention_args.restype = c_int64
+    lib.tv_sizeof_tree_attention_args.argtypes = []
+    lib.tv_store_kvcache.restype = c_int32
+    lib.tv_store_kvcache.argtypes = [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64,
+                                     c_void_p, c_int32, c_int64, c_int64, c_int32, c_void_p, c_void_p]
+    lib.tv_copy_accepted_kv_workspace_bytes.restype = c_int64
+    lib.tv_copy_accepted_kv_workspace_bytes.argtypes = [c_int64, c_int64, c_int64, c_int32]
+    lib.tv_copy_accepted_kv.restype = c_int32
+    lib.tv_copy_accepted_kv.argtypes = [c_void_p, POINTER(c_int64), POINTER(c_int64), c_int32, c_void_p,
+                                        c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int64), c_void_p,
+                                        c_void_p]
+    lib.tv_tree_attention_plan.restype = c_int32
+    lib.tv_tree_attention_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32, c_int32,
+                                           c_int32, c_int32, POINTER(c_int32), POINTER(c_int32),
+                                           POINTER(PlanInfo)]
+    lib.tv_pack_ancestor_words.restype = c_int32
+    lib.tv_pack_ancestor_words.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                           c_int32, c_void_p, c_void_p, c_void_p]
+    lib.tv_tree_attention.restype = c_int32
+    lib.tv_tree_attention.argtypes = [POINTER(TreeAttentionArgs), c_void_p]
+
+
+def library() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError if it is absent or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIBRARY_PATH.exists():
+            raise RuntimeError(
+                f"{LIBRARY_PATH} is missing: build it with `python nano-vllm-jetspec_amd/build.py` "
+                "(there is no non-HIP fallback)")
+        lib = ctypes.CDLL(str(LIBRARY_PATH))
+        missing = [name for name in EXPORTED_SYMBOLS if not hasattr(lib, name)]
+        if missing:
+            raise RuntimeError(f"{LIBRARY_PATH} lacks symbols {missing}; rebuild it")
+        _declare(lib)
+        version = lib.tv_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libtreeverify ABI {version} != binding ABI {ABI_VERSION}; rebuild it")
+        if lib.tv_sizeof_tree_attention_args() != ctypes.sizeof(TreeAttentionArgs):
+            raise RuntimeError("tv_tree_attention_args layout differs between library and binding")
+        _lib = lib
+        return lib
+
+
+def check(code: int, what: str) -> None:
+    """Raise for a nonzero C-ABI return code, with the library's message."""
+    if code == TV_OK:
+        return
+    message = library().tv_last_error().decode(errors="replace")
+    if code in (TV_ERR_INVALID, TV_ERR_UNSUPPORTED, TV_ERR_CAPACITY):
+        raise ValueError(f"{what}: {message}")
+    raise RuntimeError(f"{what}: {message} (code {code})")

@@ -1,0 +1,282 @@
+"""Packed ragged tree-verify attention on MI355X (drop-in for paged_backend.py:240-306).
+
+Every public entry keeps the reference's signature, argument meaning and ValueError
+conditions, and runs ONE hand-written HIP kernel (libtreeverify: tv_tree_attention).
+The reference's numerical variants (frozen FP32 ``reference``, ``prefix``, grouped
+``gqa``) differ only in tiling and precision knobs; here they are one kernel with
+bf16/f16 MFMA products, fp32 accumulation and online softmax, and probabilities
+rounded to the operand type for the P.V product (as the reference's gqa backend,
+tree_gqa.py:102-105).
+
+Per metadata object the wrapper derives, once, on the launch stream:
+  * the work plan (tv_tree_attention_plan over the host prefix/node counts),
+  * the ancestor bit rows (tv_pack_ancestor_words over qq_bias),
+so the 36 per-layer launches of one verify round reuse them.  A launch allocates
+only its output and (when the plan splits prefixes) a partial-result workspace.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+import weakref
+
+import numpy as np
+import torch
+
+from . import _device, _lib
+
+_BACKENDS = ("auto", "reference", "prefix", "gqa")
+_derived: dict[int, dict] = {}
+_derived_lock = threading.Lock()
+
+
+def _validate(q, k_pool, v_pool, metadata, groups, output_dtype) -> torch.dtype:
+    """Geometry/device/dtype checks of tree_attention.py:21-37; returns the output dtype."""
+    if q.ndim != 3 or q.shape[0] != metadata.total_queries:
+        raise ValueError("packed queries do not match the metadata")
+    if k_pool.ndim != 4 or k_pool.shape != v_pool.shape or k_pool.shape[1] != metadata.block_size:
+        raise ValueError("packed K/V page geometry does not match metadata")
+    if (not q.is_cuda or q.device != k_pool.device or q.device != v_pool.device
+            or q.device != metadata.tree_slots.device):
+        raise ValueError("packed attention requires CUDA queries, KV and metadata on one device")
+    if q.stride(-1) != 1 or k_pool.shape[-1] != q.shape[-1]:
+        raise ValueError("unsupported packed query/KV head geometry")
+    if isinstance(groups, bool) or not isinstance(groups, int) or groups <= 0 or q.shape[1] != k_pool.shape[2] * groups:
+        raise ValueError("invalid packed GQA head grouping")
+    if q.dtype != k_pool.dtype or k_pool.dtype != v_pool.dtype or q.dtype not in (
+            torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("packed Q/K/V must use one supported floating dtype")
+    dtype = q.dtype if output_dtype is None else output_dtype
+    if dtype not in (q.dtype, torch.float32):
+        raise ValueError("output dtype must match input or be FP32 for qualification")
+    if q.dtype == torch.float32:
+        raise ValueError("the MI355X tree-attention kernel takes bf16 or f16 operands (FP32 Q/K/V unsupported)")
+    if groups != 4 or q.shape[-1] != 128:
+        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 4 query heads per KV head")
+    if metadata.block_size % 32:
+        raise ValueError("the MI355X tree-attention kernel needs a page size that is a multiple of 32")
+    return dtype
+
+
+_METADATA_LAYOUT = (
+    ("cu_seqlens_q", torch.int32), ("query_to_request", torch.int32), ("query_local_row", torch.int32),
+    ("prefix_lens", torch.int32), ("tree_slots", torch.int64), ("qq_bias", torch.float32),
+    ("qq_bias_offsets", torch.int64), ("node_counts", torch.int32),
+)
+
+
+def _check_metadata_buffers(metadata) -> None:
+    """The kernel reads these buffers raw: dtypes, 1-D contiguity and sizes must hold."""
+    r, q = metadata.num_requests, metadata.total_queries
+    sizes = {"cu_seqlens_q": r + 1, "query_to_request": q, "query_local_row": q, "prefix_lens": r,
+             "tree_slots": q, "qq_bias_offsets": r + 1, "node_counts": r,
+             "qq_bias": sum(n * n for n in metadata.node_counts_host)}
+    for name, dtype in _METADATA_LAYOUT:
+        t = getattr(metadata, name)
+        if t.dtype != dtype or t.ndim != 1 or not t.is_contiguous() or t.numel() != sizes[name]:
+            raise ValueError(f"metadata.{name} must be a contiguous {dtype} vector of {sizes[name]} entries")
+    tables = metadata.block_tables
+    width = max(1, max(len(t) for t in metadata.block_tables_host))
+    if (tables.dtype != torch.int32 or tables.ndim != 2 or tables.shape[0] != r or tables.shape[1] < width
+            or tables.stride(1) != 1):
+        raise ValueError("metadata.block_tables must be int32 [requests, pages] with unit column stride")
+
+
+def _release(key: int) -> None:
+    with _derived_lock:
+        _derived.pop(key, None)
+
+
+def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
+    """Work plan and ancestor bits of `metadata` for `num_kv_heads`, built once per object."""
+    key = id(metadata)
+    with _derived_lock:
+        per_meta = _derived.get(key)
+    if per_meta is None:
+        _check_metadata_buffers(metadata)
+        with _derived_lock:
+            per_meta = _derived.setdefault(key, {})
+        weakref.finalize(metadata, _release, key)
+    lib = _lib.library()
+    device = metadata.tree_slots.device
+    words = per_meta.get("ancestor_words")
+    if words is None:
+        count = max(metadata.node_counts_host)
+        per_row = (count + 63) // 64
+        total = metadata.total_queries
+        words = torch.empty((max(total, 1), per_row), dtype=torch.int64, device=device)
+        status = _device.status_word(device)
+        _lib.check(lib.tv_pack_ancestor_words(
+            metadata.qq_bias.data_ptr(), metadata.qq_bias_offsets.data_ptr(),
+            metadata.query_to_request.data_ptr(), metadata.query_local_row.data_ptr(),
+            metadata.node_counts.data_ptr(), total, metadata.num_requests, per_row,
+            words.data_ptr(), status.data_ptr(), _device.stream_handle(device)), "pack_ancestor_words")
+        per_meta["ancestor_words"] = words
+        per_meta["words_per_row"] = per_row
+    plan_key = ("plan", int(num_kv_heads), int(chunk_keys))
+    plan = per_meta.get(plan_key)
+    if plan is None:
+        plan = make_plan(metadata.prefix_lengths, metadata.node_counts_host, num_kv_heads, metadata.block_size,
+                         _device.compute_units(device.index), chunk_keys)
+        plan["items_dev"] = torch.from_numpy(plan["items"]).to(device, non_blocking=False)
+        plan["groups_dev"] = (torch.from_numpy(plan["groups"]).to(device, non_blocking=False)
+                              if plan["num_groups"] else None)
+        per_meta[plan_key] = plan
+    return {"ancestor_words": per_meta["ancestor_words"], "words_per_row": per_meta["words_per_row"], **plan}
+
+
+def make_plan(prefix_lengths, node_counts, num_kv_heads: int, block_size: int, compute_units: int,
+              chunk_keys: int = 0) -> dict:
+    """Host work plan from tv_tree_attention_plan (items/groups as int32 [n, 8])."""
+    lib = _lib.library()
+    count = len(prefix_lengths)
+    prefixes = (ctypes.c_int32 * count)(*prefix_lengths)
+    nodes = (ctypes.c_int32 * count)(*node_counts)
+    info = _lib.PlanInfo()
+    _lib.check(lib.tv_tree_attention_plan(prefixes, nodes, count, num_kv_heads, block_size, compute_units,
+                                          chunk_keys, None, None, ctypes.byref(info)), "tree_attention_plan")
+    items = np.zeros((max(info.num_items, 1), 8), dtype=np.int32)
+    groups = np.zeros((max(info.num_groups, 1), 8), dtype=np.int32)
+    _lib.check(lib.tv_tree_attention_plan(
+        prefixes, nodes, count, num_kv_heads, block_size, compute_units, chunk_keys,
+        items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+        ctypes.byref(info)), "tree_attention_plan")
+    return {"items": items[:info.num_items], "groups": groups[:info.num_groups],
+            "num_items": info.num_items, "num_groups": info.num_groups,
+            "num_partial_slots": info.num_partial_slots, "workspace_bytes": int(info.workspace_bytes)}
+
+
+def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> torch.Tensor:
+    lib = _lib.library()
+    device = q.device
+    num_kv_heads = int(k_pool.shape[2])
+    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    state = derived_state(metadata, num_kv_heads, chunk_keys=chunk_keys)
+    workspace = None
+    if state["workspace_bytes"]:
+        workspace = torch.empty(state["workspace_bytes"], dtype=torch.uint8, device=device)
+    a = _lib.TreeAttentionArgs()
+    a.q = q.data_ptr()
+    a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
+    a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
+    for i in range(4):
+        a.k_stride[i] = k_pool.stride(i)
+        a.v_stride[i] = v_pool.stride(i)
+    a.num_blocks = int(k_pool.shape[0])
+    a.in_dtype = _device.dtype_code(q.dtype)
+    a.out = out.data_ptr()
+    a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
+    a.out_dtype = _device.dtype_code(out.dtype)
+    a.cu_seqlens_q = metadata.cu_seqlens_q.data_ptr()
+    a.prefix_lens = metadata.prefix_lens.data_ptr()
+    a.node_counts = metadata.node_counts.data_ptr()
+    a.block_tables = metadata.block_tables.data_ptr()
+    a.block_table_stride = metadata.block_tables.stride(0)
+    a.tree_slots = metadata.tree_slots.data_ptr()
+    a.ancestor_words = state["ancestor_words"].data_ptr()
+    a.ancestor_words_per_row = state["words_per_row"]
+    a.num_requests = metadata.num_requests
+    a.total_queries = metadata.total_queries
+    a.num_q_heads = int(q.shape[1])
+    a.num_kv_heads = num_kv_heads
+    a.head_dim = int(q.shape[2])
+    a.block_size = metadata.block_size
+    a.scale = float(scale)
+    a.items = state["items_dev"].data_ptr()
+    a.num_items = state["num_items"]
+    a.groups = state["groups_dev"].data_ptr() if state["groups_dev"] is not None else None
+    a.num_groups = state["num_groups"]
+    a.num_partial_slots = state["num_partial_slots"]
+    a.workspace = workspace.data_ptr() if workspace is not None else None
+    a.workspace_bytes = state["workspace_bytes"]
+    a.status = _device.status_word(device).data_ptr()
+    _lib.check(lib.tv_tree_attention(ctypes.byref(a), _device.stream_handle(device)), "tree_attention")
+    return out
+
+
+def packed_tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, metadata, scale: float,
+                          num_queries_per_kv: int, *, backend: str = "auto",
+                          output_dtype: torch.dtype | None = None, chunk_keys: int = 0) -> torch.Tensor:
+    """One ragged launch with independent request/ancestor visibility (paged_backend.py:240-306).
+
+    ``backend`` accepts the reference's names; all select the one HIP kernel.
+    ``chunk_keys`` (extension, default automatic) fixes the prefix split length.
+    """
+    if backend not in _BACKENDS:
+        raise ValueError("tree attention backend must be auto, reference, prefix or gqa")
+    if q.ndim != 3 or q.shape[0] != metadata.total_queries:
+        raise ValueError("packed queries do not match the metadata")
+    if k_pool.ndim != 4 or k_pool.shape != v_pool.shape or k_pool.shape[1] != metadata.block_size:
+        raise ValueError("packed K/V page geometry does not match metadata")
+    if (not q.is_cuda or q.device != k_pool.device or q.device != v_pool.device
+            or q.device != metadata.tree_slots.device):
+        raise ValueError("packed attention requires CUDA queries, KV and metadata on one device")
+    if q.stride(-1) != 1 or k_pool.shape[3] != q.shape[2]:
+        raise ValueError("unsupported packed query/KV head geometry")
+    if num_queries_per_kv <= 0 or q.shape[1] != k_pool.shape[2] * num_queries_per_kv:
+        raise ValueError("invalid packed GQA head grouping")
+    if output_dtype not in (None, q.dtype, torch.float32):
+        raise ValueError("output dtype must match input or be FP32 for qualification")
+    dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
+    out = torch.empty(q.shape, dtype=dtype, device=q.device)
+    return _launch(q, k_pool, v_pool, metadata, scale, out, chunk_keys=chunk_keys)
+
+
+def packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,
+                                    output_dtype=None):
+    """Entry of tree_attention.py:40-62 (explicit FP32 output supported)."""
+    dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
+    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device))
+
+
+def packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *, output_dtype=None,
+                              query_tile=4, prefix_scalar=True, prune=True, fp32_probability=False, num_warps=4):
+    """Entry of tree_gqa.py:114-140; the tiling switches are accepted and fixed by the kernel."""
+    if isinstance(query_tile, bool) or query_tile not in (1, 2, 4):
+        raise ValueError("GQA query tile must be 1, 2 or 4")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("grouped Tensor Core tree attention requires BF16 or FP16")
+    if num_queries_per_kv not in (1, 2, 4, 8, 16):
+        raise ValueError("grouped tree attention requires power-of-two GQA <=16")
+    dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
+    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device))
+
+
+def packed_tree_attention_register_tuned(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,
+                                         output_dtype=None, maxnreg=96):
+    """Entry of tree_attention.py:170-203; the register cap is a CUDA knob with no meaning here."""
+    if isinstance(maxnreg, bool) or maxnreg not in (64, 80, 96, 112, 128):
+        raise ValueError("maxnreg must be 64, 80, 96, 112 or 128")
+    return packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
+                                           output_dtype=output_dtype)
+
+
+def packed_tree_attention_prefix_split_exact(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,
+                                             output_dtype=None, num_warps=4):
+    """Entry of tree_prefix.py:444-463."""
+    if isinstance(num_warps, bool) or num_warps not in (4, 8, 16):
+        raise ValueError("num_warps must be 4, 8 or 16")
+    return packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
+                                           output_dtype=output_dtype)
+
+
+def packed_tree_attention_prefix_prevalidated(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, out, *,
+                                              num_warps=4):
+    """Launch-only serving entry (tree_prefix.py:466-492): caller validated and allocated `out`."""
+    return _launch(q, k_pool, v_pool, metadata, scale, out)
+
+
+def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_k, qq_bias, scale,
+                         num_queries_per_kv, block_size, logical_kv_slots=None, logical_kv_starts=None,
+                         logical_kv_lens=None):
+    """Legacy single-request entry (paged_backend.py:309-415).
+
+    Multi-request calls are rejected exactly as in the reference.  The legacy
+    logical-slot addressing (a history-sized slot vector instead of page tables)
+    is not implemented by this build: callers use PackedTreeMetadata.
+    """
+    if int(seq_lens_k.shape[0]) != 1:
+        raise ValueError("multi-request tree verification requires explicit PackedTreeMetadata")
+    raise ValueError("legacy logical-slot tree attention is not part of the MI355X build; "
+                     "build PackedTreeMetadata and call packed_tree_attention")

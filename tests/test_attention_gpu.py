@@ -1,0 +1,230 @@
+"""Tree-verify attention on the GPU vs the fp64 oracle (runs the HIP kernel via the C ABI).
+
+Gate (north star): bf16 output within max-abs 2e-2 and mean-abs 2e-3 of the fp64
+oracle; invariants (isolation, off-branch, determinism, packed == per-request,
+FP32-output round trip) are bitwise.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_helpers import assert_within_gate, oracle_rows
+from jetspec_amd import (PackedTreeMetadata, packed_tree_attention, packed_tree_attention_prefix_prevalidated,
+                         read_and_clear_status, workloads)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bits_equal(a: torch.Tensor, b: torch.Tensor) -> bool:
+    return a.dtype == b.dtype and a.shape == b.shape and torch.equal(
+        a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
+
+
+def heap_parents(n):
+    return [-1] + [(i - 1) // 2 for i in range(1, n)]
+
+
+def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dtype=torch.bfloat16, seed=317):
+    """The reference GPU fixture geometry (tests/test_jetspec_packed_attention.py:109-125) with
+    shuffled pages, scattered scratch slots and NaN in every unused pool row."""
+    rng = np.random.default_rng(seed)
+    block = 256
+    prefix_pages = [-(-p // block) for p in prefixes]
+    scratch_pages = -(-sum(counts) // block) + 1
+    total = sum(prefix_pages) + scratch_pages + 3
+    order = rng.permutation(total)
+    tables, cursor = [], 0
+    for n in prefix_pages:
+        tables.append([int(x) for x in order[cursor:cursor + n]])
+        cursor += n
+    scratch = order[cursor:cursor + scratch_pages]
+    pool_slots = (scratch[:, None] * block + np.arange(block)).reshape(-1)[rng.permutation(scratch_pages * block)]
+    slots, parents, off = [], [], 0
+    for i, n in enumerate(counts):
+        slots.append(torch.as_tensor(pool_slots[off:off + n].astype(np.int64), device=DEV))
+        parents.append(workloads.random_parents(n, 8, rng) if i % 2 else heap_parents(n))
+        off += n
+    masks = [torch.as_tensor(workloads.ancestor_mask(p), device=DEV) for p in parents]
+    meta = PackedTreeMetadata.build(list(prefixes), tables, slots, masks, block)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    k = torch.full((total, block, kv_heads, 128), float("nan"), device=DEV, dtype=dtype)
+    v = torch.full_like(k, float("nan"))
+    live = [torch.as_tensor(np.asarray(t, dtype=np.int64)[np.arange(p) // block] * block + np.arange(p) % block,
+                            device=DEV) for t, p in zip(tables, prefixes)]
+    live = torch.cat(live + slots)
+    k.view(-1, kv_heads, 128)[live] = torch.randn((live.numel(), kv_heads, 128), generator=gen, device=DEV).to(dtype)
+    v.view(-1, kv_heads, 128)[live] = torch.randn((live.numel(), kv_heads, 128), generator=gen, device=DEV).to(dtype)
+    q = torch.randn((meta.total_queries, kv_heads * 4, 128), generator=gen, device=DEV).to(dtype)
+    return q, k, v, meta, slots, masks, parents
+
+
+def check_all_rows(q, k, v, meta, label, **kwargs):
+    out = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4, **kwargs)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item(), f"{label}: NaN padding was read"
+    expect = oracle_rows(q, k, v, meta, 128 ** -0.5, list(range(meta.num_requests)))
+    assert_within_gate(out, expect, label)
+    assert read_and_clear_status(q.device) == 0
+    return out
+
+
+def test_config1_all_rows_match_oracle():
+    batch = workloads.config1(DEV)
+    check_all_rows(batch.q, batch.k_pool, batch.v_pool, batch.metadata, "cfg1")
+
+
+def test_reference_fixture_nan_poisoned_pool():
+    q, k, v, meta, *_ = reference_fixture()
+    check_all_rows(q, k, v, meta, "fixture(63,31,47)")
+
+
+@pytest.mark.parametrize("prefix", [0, 1, 63, 64, 65, 255, 256, 257, 1024, 2048])
+def test_boundary_prefixes(prefix):
+    q, k, v, meta, *_ = reference_fixture(prefixes=(prefix, 0, max(0, prefix - 1)))
+    check_all_rows(q, k, v, meta, f"prefix={prefix}")
+
+
+def test_config2_all_rows_match_oracle():
+    batch = workloads.config2(DEV)
+    check_all_rows(batch.q, batch.k_pool, batch.v_pool, batch.metadata, "cfg2")
+
+
+@pytest.mark.parametrize("chunk", [32, 96, 256, 1024])
+def test_forced_prefix_splits_match_oracle(chunk):
+    batch = workloads.config2(DEV, seed=12)
+    check_all_rows(batch.q, batch.k_pool, batch.v_pool, batch.metadata, f"cfg2 chunk={chunk}", chunk_keys=chunk)
+
+
+def test_fp16_operands():
+    q, k, v, meta, *_ = reference_fixture(prefixes=(300, 17, 700), counts=(40, 9, 64), dtype=torch.float16)
+    check_all_rows(q, k, v, meta, "fp16")
+
+
+def test_fp32_output_round_trips_to_bf16_output_and_repeat_is_bitwise():
+    q, k, v, meta, *_ = reference_fixture(prefixes=(1000, 33, 513))
+    out = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    out32 = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4, output_dtype=torch.float32)
+    again = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    assert out32.dtype == torch.float32
+    assert bits_equal(out32.to(torch.bfloat16), out)
+    assert bits_equal(out, again)
+    pre = torch.empty_like(q)
+    packed_tree_attention_prefix_prevalidated(q, k, v, meta, 128 ** -0.5, 4, pre)
+    assert bits_equal(pre, out)
+
+
+def test_other_requests_cannot_affect_neighbors():
+    q, k, v, meta, slots, masks, _ = reference_fixture()
+    original = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    cq, ck, cv = q.clone(), k.clone(), v.clone()
+    cq[meta.request_slice(0)] *= 31
+    table = meta.block_tables_host[0]
+    pos = torch.arange(meta.prefix_lengths[0], device=DEV)
+    prefix_slots = torch.as_tensor(table, device=DEV)[pos // 256] * 256 + pos % 256
+    changed = torch.cat((prefix_slots, slots[0]))
+    ck.view(-1, 2, 128)[changed] *= -17
+    cv.view(-1, 2, 128)[changed] += 53
+    result = packed_tree_attention(cq, ck, cv, meta, 128 ** -0.5, 4)
+    for neighbor in (1, 2):
+        assert bits_equal(result[meta.request_slice(neighbor)], original[meta.request_slice(neighbor)])
+    assert not torch.equal(result[meta.request_slice(0)], original[meta.request_slice(0)])
+
+
+def test_off_branch_changes_do_not_affect_ancestor_path():
+    q, k, v, meta, slots, masks, _ = reference_fixture()
+    original = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    ancestors = masks[0][55]
+    ck, cv = k.clone(), v.clone()
+    off_path = slots[0][~ancestors]
+    ck.view(-1, 2, 128)[off_path] *= 97
+    cv.view(-1, 2, 128)[off_path] += 113
+    result = packed_tree_attention(q, ck, cv, meta, 128 ** -0.5, 4)
+    assert bits_equal(result[:63][ancestors], original[:63][ancestors])
+
+
+def test_packed_equals_per_request_launches():
+    q, k, v, meta, slots, masks, _ = reference_fixture(prefixes=(700, 0, 257), counts=(63, 31, 47))
+    packed = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4, chunk_keys=256)
+    for r in range(3):
+        solo = PackedTreeMetadata.build([meta.prefix_lengths[r]], [meta.block_tables_host[r]], [slots[r]],
+                                        [masks[r]], 256)
+        out = packed_tree_attention(q[meta.request_slice(r)].contiguous(), k, v, solo, 128 ** -0.5, 4,
+                                    chunk_keys=256)
+        assert bits_equal(out, packed[meta.request_slice(r)]), f"request {r}"
+
+
+def test_strided_query_view():
+    q, k, v, meta, *_ = reference_fixture(prefixes=(129, 5, 400))
+    wide = torch.zeros((q.shape[0], q.shape[1] + 4, 128), dtype=q.dtype, device=DEV)
+    wide[:, 2:2 + q.shape[1]] = q
+    view = wide[:, 2:2 + q.shape[1]]
+    assert not view.is_contiguous()
+    assert bits_equal(packed_tree_attention(view, k, v, meta, 128 ** -0.5, 4),
+                      packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4))
+
+
+def test_rejections_match_reference_contract():
+    q, k, v, meta, *_ = reference_fixture()
+    with pytest.raises(ValueError, match="backend"):
+        packed_tree_attention(q, k, v, meta, 0.1, 4, backend="triton")
+    with pytest.raises(ValueError, match="metadata"):
+        packed_tree_attention(q[:-1], k, v, meta, 0.1, 4)
+    with pytest.raises(ValueError, match="grouping"):
+        packed_tree_attention(q, k, v, meta, 0.1, 2)
+    with pytest.raises(ValueError, match="output dtype"):
+        packed_tree_attention(q, k, v, meta, 0.1, 4, output_dtype=torch.float16)
+    with pytest.raises(ValueError, match="CUDA"):
+        packed_tree_attention(q.cpu(), k, v, meta, 0.1, 4)
+
+
+@pytest.mark.parametrize("config", ["config4", "config5"])
+def test_large_configs_sampled_rows(config):
+    batch = getattr(workloads, config)(DEV)
+    out = packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, batch.metadata, batch.scale, 4)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item()
+    meta = batch.metadata
+    rng = np.random.default_rng(0)
+    requests = sorted(rng.choice(meta.num_requests, size=6, replace=False).tolist())
+    if config == "config5":
+        requests = sorted(set(requests) | {int(np.argmax(meta.prefix_lengths[:16]))})
+    expect = oracle_rows(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, requests, rows_per_request=4)
+    assert_within_gate(out, expect, f"{config} sampled rows")
+    assert read_and_clear_status(batch.q.device) == 0
+
+
+def test_greedy_acceptance_identical_to_oracle():
+    """Project outputs through one seeded vocab head; argmax flips only where the oracle's
+    top-2 margin is within 2 * sup error (jetspec_numeric_oracles.py:171-217), and the
+    accepted paths of every request agree."""
+    batch = workloads.config2(DEV, seed=21)
+    meta = batch.metadata
+    out = packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, 4)
+    expect = oracle_rows(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, list(range(meta.num_requests)))
+    head = torch.randn((32 * 128, 512), generator=torch.Generator().manual_seed(7), dtype=torch.float64)
+    got = out.double().cpu().reshape(out.shape[0], -1) @ head
+    ref = torch.zeros_like(got)
+    for rows, values in expect.values():
+        ref[rows] = torch.from_numpy(values.reshape(values.shape[0], -1)) @ head
+    witness = oracle.argmax_flip_witness(got.numpy(), ref.numpy())
+    print(f"[acceptance] rows {witness['rows_checked']} flips {witness['argmax_flips']} "
+          f"violations {witness['large_margin_violations']}", flush=True)
+    assert witness["large_margin_violations"] == 0
+    rng = np.random.default_rng(3)
+    greedy_gpu, greedy_ref = got.argmax(-1).tolist(), ref.argmax(-1).tolist()
+    for r, parents in enumerate(batch.parents):
+        sl = meta.request_slice(r)
+        tokens = [int(t) for t in rng.integers(0, 512, size=len(parents))]
+        # make the tree follow the oracle's greedy choice so long paths are exercised
+        for node in range(1, len(parents)):
+            tokens[node] = greedy_ref[sl.start + parents[node]] if rng.random() < 0.8 else tokens[node]
+        children = oracle.child_maps(tokens, parents)
+        depths = workloads.depths_of(parents)
+        a = oracle.accept_walk(greedy_gpu[sl], tokens, depths, children, 15)
+        b = oracle.accept_walk(greedy_ref[sl], tokens, depths, children, 15)
+        if witness["argmax_flips"] == 0:
+            assert a == b, f"request {r}"

@@ -1,0 +1,125 @@
+"""The C-ABI library: loads, exports every declared symbol, and its host planner (CPU).
+
+No device call is made here (there is no GPU in the CPU suite); the work planner is
+pure host code, so its coverage invariants are checked exhaustively on CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+import re
+
+import numpy as np
+import pytest
+
+from jetspec_amd import _lib
+from jetspec_amd.paged_backend import make_plan
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "treeverify.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.library()
+    declared = declared_functions()
+    assert declared, "no declarations parsed"
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_struct_layout():
+    lib = _lib.library()
+    assert lib.tv_abi_version() == _lib.ABI_VERSION
+    assert lib.tv_sizeof_tree_attention_args() == ctypes.sizeof(_lib.TreeAttentionArgs)
+    assert lib.tv_last_error() is not None
+
+
+def test_entry_points_reject_bad_arguments_without_a_device():
+    lib = _lib.library()
+    # A null args pointer and an invalid store are rejected before any launch.
+    assert lib.tv_tree_attention(None, None) == _lib.TV_ERR_INVALID
+    assert b"null" in lib.tv_last_error()
+    assert lib.tv_store_kvcache(None, 0, None, 0, None, None, 0, None, 0, -1, 8, 2, None, None) == _lib.TV_ERR_INVALID
+    shape = (ctypes.c_int64 * 6)(3, 1, 1, 16, 1, 8)
+    stride = (ctypes.c_int64 * 6)(128, 128, 128, 8, 8, 1)
+    assert lib.tv_copy_accepted_kv(None, shape, stride, 2, None, None, 1, None, 0, None, None, None) \
+        == _lib.TV_ERR_INVALID
+    assert lib.tv_copy_accepted_kv_workspace_bytes(12, 36, 1024, 2) >= 2 * 36 * 12 * 1024 * 2
+    with pytest.raises(ValueError, match="block_size"):
+        make_plan([10], [4], 8, 48, 256)
+    with pytest.raises(ValueError, match="no tree nodes"):
+        make_plan([10], [0], 8, 256, 256)
+
+
+def heads_per_group(nodes, kv_heads):
+    h = 4 if nodes <= 16 else (2 if nodes <= 32 else 1)
+    while h > 1 and h > kv_heads:
+        h //= 2
+    return h
+
+
+def check_plan_covers(prefixes, counts, kv_heads, cus, chunk=0, block=256):
+    plan = make_plan(prefixes, counts, kv_heads, block, cus, chunk)
+    items, groups = plan["items"], plan["groups"]
+    covered = {}
+    slots_seen = set()
+    for r, h0, n0, kbeg, kend, flags, slot, hpw in items.tolist():
+        assert hpw == heads_per_group(counts[r], kv_heads)
+        assert h0 % hpw == 0 and n0 % (64 // hpw) == 0
+        assert 0 <= kbeg <= kend <= prefixes[r] and kbeg % 32 == 0
+        key = (r, h0, n0)
+        covered.setdefault(key, []).append((kbeg, kend, flags, slot))
+        if slot >= 0:
+            assert slot not in slots_seen
+            slots_seen.add(slot)
+    for r, (p, t) in enumerate(zip(prefixes, counts)):
+        hpw = heads_per_group(t, kv_heads)
+        npw = 64 // hpw
+        for h0 in range(0, kv_heads, hpw):
+            for n0 in range(0, t, npw):
+                ranges = sorted(covered.pop((r, h0, n0)))
+                # contiguous prefix coverage, tree exactly once, on the last chunk
+                assert ranges[0][0] == 0 and ranges[-1][1] == p
+                for a, b in zip(ranges, ranges[1:]):
+                    assert a[1] == b[0]
+                assert [f for _, _, f, _ in ranges] == [0] * (len(ranges) - 1) + [1]
+                if len(ranges) > 1:
+                    assert all(s >= 0 for _, _, _, s in ranges)
+                else:
+                    assert ranges[0][3] == -1
+    assert not covered
+    assert plan["num_partial_slots"] == len(slots_seen)
+    for r, h0, n0, hpw, first, ns, _, _ in groups.tolist():
+        assert set(range(first, first + ns)) <= slots_seen
+    costs = [(kend - kbeg + (t if flags else 0)) * hpw for (_, _, _, kbeg, kend, flags, _, hpw), t in
+             zip(items.tolist(), [counts[i[0]] for i in items.tolist()])]
+    assert costs == sorted(costs, reverse=True), "items must be ordered longest first"
+    return plan
+
+
+@pytest.mark.parametrize("prefixes,counts", [
+    ([512], [16]),
+    ([0, 1, 63, 64, 65, 255, 256, 257], [1, 2, 16, 17, 32, 33, 64, 65]),
+    ([4096, 300, 0], [512, 31, 64]),
+])
+@pytest.mark.parametrize("kv_heads", [1, 2, 8])
+@pytest.mark.parametrize("chunk", [0, 32, 256])
+def test_plan_covers_every_row_and_key_once(prefixes, counts, kv_heads, chunk):
+    check_plan_covers(prefixes, counts, kv_heads, 256, chunk)
+
+
+def test_plan_at_benchmark_shapes():
+    rng = np.random.default_rng(4)
+    prefixes = [int(x) for x in rng.integers(8192, 32769, size=64)]
+    plan = check_plan_covers(prefixes, [64] * 64, 8, 256)
+    assert plan["num_groups"] == 0, "long contexts fill the chip without split-K"
+    rng = np.random.default_rng(2)
+    prefixes = [int(x) for x in rng.integers(256, 4097, size=8)]
+    plan = check_plan_covers(prefixes, [16, 32, 64, 16, 32, 64, 16, 32], 8, 256)
+    assert plan["num_items"] >= 128, "short batches are split to occupy the chip"

@@ -1,0 +1,138 @@
+"""KV append (store_kvcache) and accepted-only commit (copy_accepted_kv) on the GPU.
+
+Bit-exact against the C oracle at sizes it handles in seconds; at config-3 size
+(36 layers, ~52 GB pool) through size-independent properties: destination rows
+equal the pre-commit source rows and every other byte of the pool is unchanged.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jetspec_amd import copy_accepted_kv, read_and_clear_status, store_kvcache, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def as_bytes(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().cpu().view(torch.uint8).numpy()
+
+
+def test_tree_append_config1_bit_exact():
+    batch = workloads.config1(DEV)
+    k_pool, v_pool = batch.k_pool.clone(), batch.v_pool.clone()
+    k_pool.view(-1, 8, 128)[batch.metadata.tree_slots] = float("nan")
+    v_pool.view(-1, 8, 128)[batch.metadata.tree_slots] = float("nan")
+    k_ref, v_ref = as_bytes(k_pool).copy(), as_bytes(v_pool).copy()
+    store_kvcache(batch.new_k, batch.new_v, k_pool, v_pool, batch.metadata.tree_slots)
+    torch.cuda.synchronize()
+    oracle.store_kvcache(as_bytes(batch.new_k), as_bytes(batch.new_v), k_ref, v_ref,
+                         batch.metadata.tree_slots.cpu().numpy())
+    assert np.array_equal(as_bytes(k_pool), k_ref)
+    assert np.array_equal(as_bytes(v_pool), v_ref)
+    assert read_and_clear_status(DEV) == 0
+
+
+@pytest.mark.parametrize("slot_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_store_with_skips_strided_rows_and_bad_slots(slot_dtype, dtype):
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    qkv = torch.randn((300, 48, 128), generator=gen, device=DEV).to(dtype)
+    key, value = qkv[:, 32:40], qkv[:, 40:48]          # strided views, as after a fused QKV split
+    k_cache = torch.randn((7, 256, 8, 128), generator=gen, device=DEV).to(dtype)
+    v_cache = torch.randn((7, 256, 8, 128), generator=gen, device=DEV).to(dtype)
+    rng = np.random.default_rng(1)
+    slots = rng.permutation(7 * 256)[:300].astype(np.int64)
+    slots[rng.choice(300, 40, replace=False)] = -1
+    slots[7] = 7 * 256 + 3          # outside the cache: skipped and reported
+    k_ref, v_ref = as_bytes(k_cache).copy(), as_bytes(v_cache).copy()
+    mapping = torch.as_tensor(slots, device=DEV).to(slot_dtype)
+    store_kvcache(key, value, k_cache, v_cache, mapping)
+    torch.cuda.synchronize()
+    assert read_and_clear_status(DEV) == 2
+    valid = slots.copy()
+    valid[7] = -1
+    oracle.store_kvcache(as_bytes(key.contiguous()).reshape(300, -1), as_bytes(value.contiguous()).reshape(300, -1),
+                         k_ref, v_ref, valid)
+    assert np.array_equal(as_bytes(k_cache), k_ref)
+    assert np.array_equal(as_bytes(v_cache), v_ref)
+
+
+def test_store_contract_assertions():
+    k_cache = torch.zeros((2, 256, 8, 128), dtype=torch.bfloat16, device=DEV)
+    key = torch.zeros((4, 8, 128), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(AssertionError):
+        store_kvcache(key, key, k_cache, k_cache, torch.zeros(3, dtype=torch.int64, device=DEV))
+    with pytest.raises(AssertionError):
+        store_kvcache(key.transpose(1, 2), key.transpose(1, 2), k_cache, k_cache,
+                      torch.zeros(4, dtype=torch.int64, device=DEV))
+
+
+def small_commit_case(seed, overlap=False, layers=4):
+    rng = np.random.default_rng(seed)
+    pool = torch.randn((2, layers, 12, 256, 8, 128), generator=torch.Generator(device=DEV).manual_seed(seed),
+                       device=DEV).to(torch.bfloat16)
+    slots = rng.permutation(12 * 256)
+    src, dst = slots[:200], slots[200:400]
+    if overlap:
+        dst = dst.copy()
+        dst[::3] = src[rng.permutation(200)[:len(dst[::3])]]
+    return pool, src.astype(np.int64), dst.astype(np.int64)
+
+
+@pytest.mark.parametrize("overlap", [False, True])
+def test_commit_bit_exact_against_oracle(overlap):
+    pool, src, dst = small_commit_case(11, overlap)
+    expect = as_bytes(pool).copy().view(np.uint16).reshape(pool.shape)
+    payload = copy_accepted_kv(pool, torch.as_tensor(src, device=DEV), torch.as_tensor(dst, device=DEV), 256)
+    torch.cuda.synchronize()
+    assert payload == 200 * 2 * 4 * 8 * 128 * 2
+    assert oracle.copy_accepted_kv(expect, src, dst) == payload
+    assert np.array_equal(as_bytes(pool), expect.view(np.uint8).reshape(-1))
+    assert read_and_clear_status(DEV) == 0
+
+
+def test_commit_contract():
+    pool, src, dst = small_commit_case(3)
+    s = torch.as_tensor(src, device=DEV)
+    with pytest.raises(ValueError, match="one-dimensional"):
+        copy_accepted_kv(pool, s.view(2, -1), s.view(2, -1), 256)
+    with pytest.raises(ValueError, match="lengths differ"):
+        copy_accepted_kv(pool, s, s[:-1], 256)
+    assert copy_accepted_kv(pool, s[:0], s[:0], 256) == 0
+    bad = torch.as_tensor(dst, device=DEV).clone()
+    bad[4] = 12 * 256 + 9
+    before = pool.clone()
+    copy_accepted_kv(pool, s, bad, 256)
+    torch.cuda.synchronize()
+    assert read_and_clear_status(DEV) == 2
+    assert torch.equal(pool.view(torch.int16), before.view(torch.int16)), "an invalid map must not write"
+
+
+def test_config3_commit_full_size_properties():
+    batch = workloads.config3(DEV)
+    pool, src, dst = batch.kv_pool, batch.source, batch.destination
+    print(f"[cfg3] pool {tuple(pool.shape)} rows {src.numel()} "
+          f"payload {2 * pool.shape[1] * src.numel() * 2048 / 1e6:.1f} MB", flush=True)
+    block = pool.shape[3]
+    flat = pool.view(2, pool.shape[1], -1, 8, 128)
+    expected_rows = flat[:, :, src].clone()
+    dst_set = set(dst.tolist())
+    assert not dst_set & set(src.tolist())
+    # checksum of every slot row before the commit, per (kv, layer)
+    def row_sums():
+        return torch.stack([flat[kv, layer].view(torch.int16).view(-1, 1024).to(torch.int32).sum(1)
+                            for kv in range(2) for layer in range(pool.shape[1])])
+    before = row_sums()
+    payload = copy_accepted_kv(pool, src, dst, block)
+    torch.cuda.synchronize()
+    assert payload == 2 * pool.shape[1] * src.numel() * 8 * 128 * 2
+    assert bool(torch.equal(flat[:, :, dst].view(torch.int16), expected_rows.view(torch.int16)))
+    after = row_sums()
+    untouched = torch.ones(before.shape[1], dtype=torch.bool, device=DEV)
+    untouched[dst] = False
+    assert bool(torch.equal(before[:, untouched], after[:, untouched]))
+    assert read_and_clear_status(DEV) == 0

@@ -1,0 +1,54 @@
+"""Greedy acceptance (host walk): reference KAT and agreement with the oracle walk (CPU)."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import torch
+
+import oracle
+from jetspec_amd import accept_batch, build_child_maps, workloads
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+def test_duplicate_sibling_kat_last_child_wins():
+    kat = KATS["accept_duplicate_siblings"]
+    tree = SimpleNamespace(token_ids=torch.tensor(kat["tokens"]), parent_indices=torch.tensor(kat["parents"]),
+                           depth=torch.tensor(kat["depths"]), num_nodes=len(kat["tokens"]))
+    logits = torch.randn(len(kat["tokens"]), 80, generator=torch.Generator().manual_seed(99))
+    for node, token in kat["forced_argmax"].items():
+        logits[int(node), token] = 100
+    result = accept_batch(logits, [tree], [0, len(kat["tokens"])], kat["max_depth"])[0]
+    assert result["path"] == kat["expected_path"]
+    assert result["accepted_length"] == len(kat["expected_path"]) - 1
+    assert result["correction"] == int(logits[kat["expected_path"][-1]].argmax())
+    assert result["outputs"] == [kat["tokens"][n] for n in kat["expected_path"][1:]] + [result["correction"]]
+
+
+def test_child_maps_match_oracle_rule():
+    rng = np.random.default_rng(4)
+    for n in (1, 5, 33, 64):
+        parents = workloads.random_parents(n, 8, rng)
+        tokens = [int(t) for t in rng.integers(0, 6, size=n)]
+        assert build_child_maps(tokens, parents) == oracle.child_maps(tokens, parents)
+
+
+def test_batch_walks_equal_oracle_walks_with_host_topology():
+    rng = np.random.default_rng(5)
+    trees, offsets = [], [0]
+    for n in (1, 16, 31, 64):
+        parents = workloads.random_parents(n, 8, rng)
+        tokens = [int(t) for t in rng.integers(0, 5, size=n)]
+        trees.append(SimpleNamespace(num_nodes=n, host_token_ids=tokens, host_depths=workloads.depths_of(parents),
+                                     child_maps=oracle.child_maps(tokens, parents), parents=parents))
+        offsets.append(offsets[-1] + n)
+    logits = torch.from_numpy(rng.standard_normal((offsets[-1], 5)).astype(np.float32))
+    results = accept_batch(logits, trees, offsets, 15)
+    greedy = logits.argmax(-1).tolist()
+    for i, tree in enumerate(trees):
+        expected = oracle.accept_walk(greedy[offsets[i]:offsets[i + 1]], tree.host_token_ids, tree.host_depths,
+                                      tree.child_maps, 15)
+        assert results[i] == expected
