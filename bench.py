@@ -110,6 +110,26 @@ def cpu_baseline(batch, requests: int) -> dict:
                       f"median of 3 after 1 warmup, samples_s={[round(s, 3) for s in samples]}"}
 
 
+def copy_probe(torch, gib: int = 2, reps: int = 10) -> dict:
+    """Device-to-device copy of a known size: the measured HBM ceiling next to the 8 TB/s
+    vendor peak, and the reference kernel for calibrating rocprofv3 FETCH/WRITE_SIZE."""
+    n = gib << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    del src, dst
+    return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9}
+
+
 def run_verify(args, torch):
     from jetspec_amd import packed_tree_attention, read_and_clear_status, store_kvcache, workloads
 
@@ -164,6 +184,9 @@ def run_verify(args, torch):
                      "achieved_tflops": batch.algorithmic_flops() / (attn_ms * 1e-3) / 1e12,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
     }
+    probe = copy_probe(torch)
+    result["roofline"]["measured_copy_gbs"] = probe["gbs"]
+    result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]
     if args.cpu_requests > 0 and args.config in (1, 2, 4, 5):
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_requests)
     return result
@@ -192,6 +215,7 @@ def run_commit(args, torch):
     algo = batch.algorithmic_bytes()
     achieved = algo / (ms * 1e-3) / 1e9
     rows = int(src.numel())
+    probe = copy_probe(torch)
     return {"metric": "accepted KV rows committed/sec (36 layers) + achieved HBM GB/s", "value": rows * args.steps / elapsed,
             "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak",
@@ -199,7 +223,8 @@ def run_commit(args, torch):
             "config": {"workload": WORKLOADS[3], "accepted_rows": rows, "pool_pages": batch.info["pages"]},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes(3), "kernel_ms": ms,
-                         "algorithmic_bytes": algo}}
+                         "algorithmic_bytes": algo, "measured_copy_gbs": probe["gbs"],
+                         "frac_of_measured_copy": achieved / probe["gbs"]}}
 
 
 def main() -> int:

@@ -5,19 +5,28 @@
 // the tree nodes of r whose ancestor bit is set (scratch slot addressed), with an
 // fp32 online softmax.  GQA: query head h reads KV head h / 4.
 //
-// Work decomposition (see tv_plan.cpp): one 512-thread workgroup = 8 waves owns
-// 256 score rows = HPW KV heads x NPW nodes x 4 query heads, and a key range of the
+// Work decomposition (tv_plan.cpp): one 512-thread workgroup = 8 waves owns 256
+// score rows = HPW KV heads x NPW nodes x 4 query heads, and a key range of the
 // request (a prefix chunk, plus the tree on the last chunk).  Each wave owns 32
 // score rows (8 nodes x 4 query heads of one KV head).
 //
-// Per 32-key tile the workgroup stages K and V of its HPW heads in LDS once, and
-// every wave of a head reads them from LDS:
-//   S^T[32 keys x 32 rows]  = K  . Q^T   (8 x v_mfma_f32_32x32x16_bf16)
-//   O^T[128 dims x 32 rows] += V^T . P^T  (8 x v_mfma_f32_32x32x16_bf16)
+// Data path per 32-key tile:
+//   HBM -> VGPR   every thread loads one 16-byte chunk of K and of V per head; the
+//                 loads of the next PF tiles are in flight while a tile is computed
+//                 (PF * HPW = 4 tiles of 16 KiB per workgroup), and no address
+//                 depends on a load inside the loop: the chunk's page numbers and the
+//                 tree's slots are read into LDS once per work item.
+//   VGPR -> LDS   natural [key][dim] rows of 256 B with the 16-byte chunks XOR-
+//                 swizzled per key (K: chunk ^ key%8, V: chunk ^ 2*(key%4)), which
+//                 makes both operand reads below bank-conflict free.
+//   LDS -> MFMA   S^T[32 keys x 32 rows]  = K . Q^T   (8 x v_mfma_f32_32x32x16_bf16)
+//                 O^T[128 dims x 32 rows] += V^T . P^T (8 x v_mfma_f32_32x32x16_bf16)
+//                 K operands are ds_read_b128; V^T operands come from ds_read_b64_tr_b16
+//                 transposing reads, so V is never transposed in registers.
 // Writing the products transposed keeps every per-row quantity (running max, sum,
 // rescale factor) in the two lanes (c, c+32) that own row c: the MFMA C layout puts
 // column c in lanes c and c+32, so the softmax needs one cross-lane exchange per
-// reduction and the O^T rescale needs none.
+// reduction and the O^T rescale none.
 //
 // MFMA 32x32x16 register layouts (gfx950):
 //   A (32 x 16): lane l holds row l%32, k-slots 8*(l/32)+0..7
@@ -26,8 +35,15 @@
 // The P^T operand is taken straight from the S^T registers, so the k-slot order of
 // the P.V product is a permutation of the tile's keys:
 //   k-slot t of lane half g in product kk  <->  key 16*kk + 8*(t/4) + 4*g + t%4.
-// V is stored in LDS transposed ([dim][key], keys in that permuted order), so each
-// V^T operand is one 16-byte LDS read.
+// ds_read_b64_tr_b16 (per 16-lane group, result lane 4a+b receives element b of
+// source lanes a, a+4, a+8, a+12) delivers exactly those keys when source lane s of
+// group G reads key 16*kk + 8*h + 4*(G/2) + s/4, dims 32*db + 16*(G%2) + 4*(s%4) + 0..3.
+//
+// Softmax: scores are scaled by softmax_scale*log2(e) inside one FMA before exp2.
+// The running maximum is raised only when a tile's maximum exceeds it by more than
+// 2^8 in probability units (then O and the sum are rescaled); between raises the
+// probabilities are bounded by 2^8, which fp32 and bf16 hold exactly as well as
+// values <= 1, so the result is the same online softmax with fewer rescales.
 #include <math.h>
 #include <stdint.h>
 
@@ -40,20 +56,25 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int kHeadDim = 128;
 constexpr int kGroups = 4;          // query heads per KV head
 constexpr int kThreads = 512;       // 8 waves
 constexpr int kRowsPerItem = 256;
 constexpr int kTileKeys = 32;
-constexpr int kKRow = kHeadDim + 8;                   // bf16 per LDS K row (272 B: conflict-free reads)
-constexpr int kVRow = kTileKeys + 8;                  // bf16 per LDS V^T row (80 B: conflict-free reads)
-constexpr int kKHeadBytes = kTileKeys * kKRow * 2;    // 8704
-constexpr int kVHeadBytes = kHeadDim * kVRow * 2;     // 10240
+constexpr int kRowBytes = kHeadDim * 2;               // one K or V row of one head (bf16/f16)
+constexpr int kTileBytes = kTileKeys * kRowBytes;     // 8 KiB: K (or V) of one head, one tile
 constexpr int kMaxHpw = 4;
-constexpr int kStageBytes = kMaxHpw * (kKHeadBytes + kVHeadBytes);  // 75776
-constexpr int kLdsBytes = 2 * kStageBytes;                          // 151552 of gfx950's 160 KiB
+constexpr int kStageBytes = kMaxHpw * 2 * kTileBytes; // 64 KiB: K and V of up to 4 heads
+constexpr int kMaxPages = 512;                        // page numbers of one prefix chunk
+constexpr int kMaxTreeSlots = 1024;                   // tree slots cached per work item
+constexpr int kPagesOffset = 2 * kStageBytes;
+constexpr int kSlotsOffset = kPagesOffset + kMaxPages * 4;
+constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 137216 of gfx950's 160 KiB
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleThreshold = 8.f;              // log2 units
 
 template <typename T>
 struct Mfma;
@@ -102,46 +123,8 @@ struct AttnParams {
     int32_t* status;
 };
 
-// Element offset of key `key` of tile `t` within its page row, for K and V.
-// Returns false (and reports) when the key is outside the item's range or its
-// page lies outside the pool; such keys are neither loaded nor visible.
-struct KeyRow {
-    int64_t k_off, v_off;
-    bool valid;
-};
-
-__device__ __forceinline__ KeyRow key_row(const AttnParams& p, int r, int qbase, int kbeg, int kend, int ntp,
-                                          int tree_end, int t, int key) {
-    KeyRow out{0, 0, false};
-    int64_t page, off;
-    if (t < ntp) {
-        const int pos = kbeg + kTileKeys * t + key;
-        if (pos >= kend) return out;
-        page = p.tables[static_cast<int64_t>(r) * p.t_s0 + pos / p.block_size];
-        off = pos % p.block_size;
-    } else {
-        const int m = kTileKeys * (t - ntp) + key;
-        if (m >= tree_end) return out;
-        const int64_t slot = p.tree_slots[qbase + m];
-        if (slot < 0) {
-            set_status(p.status, TV_STATUS_BAD_PAGE);
-            return out;
-        }
-        page = slot / p.block_size;
-        off = slot - page * p.block_size;
-    }
-    if (page < 0 || page >= p.num_blocks) {
-        set_status(p.status, TV_STATUS_BAD_PAGE);
-        return out;
-    }
-    out.k_off = page * p.k_s0 + off * p.k_s1;
-    out.v_off = page * p.v_s0 + off * p.v_s1;
-    out.valid = true;
-    return out;
-}
-
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+__device__ __forceinline__ int k_swizzle(int key) { return key & 7; }
+__device__ __forceinline__ int v_swizzle(int key) { return 2 * (key & 3); }
 
 template <typename T>
 __device__ __forceinline__ void store_out4(const AttnParams& p, int64_t row, int qh, int dim, f32x4 v) {
@@ -155,34 +138,68 @@ __device__ __forceinline__ void store_out4(const AttnParams& p, int64_t row, int
     }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(kThreads)
-tree_attention_kernel(const AttnParams p) {
-    typedef typename Mfma<T>::vec V8;
-    __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+// s_waitcnt immediate that waits for vmcnt <= n and leaves expcnt/lgkmcnt alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
-    const int32_t* it = p.items + 8 * blockIdx.x;
-    const int r = it[0], h0 = it[1], n0 = it[2], kbeg = it[3], kend = it[4];
-    const int flags = it[5], slot = it[6], hpw = it[7];
-    if (r < 0 || r >= p.num_requests) {
-        if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
-        return;
-    }
+struct Item {
+    int r, h0, n0, kbeg, kend, flags, slot, hpw;
+};
+
+// One work item with HPW KV heads per workgroup.
+template <typename T, int HPW>
+__device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it) {
+    typedef typename Mfma<T>::vec V8;
+    constexpr int PF = 4 / HPW;   // tiles of K/V in flight per thread
+    constexpr int WPH = 8 / HPW;  // waves per KV head
+    constexpr int NPW = 8 * WPH;  // nodes per workgroup
+
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
-    const int wph = 8 / hpw;  // waves per KV head
-    const int npw = 8 * wph;  // nodes per workgroup
-    const int hl = wave / wph;
-    const int head = h0 + hl;
-    const int nsub = wave - hl * wph;
+    const int hl = wave / WPH;
+    const int head = it.h0 + hl;
+    const int nsub = wave - hl * WPH;
+    const int r = it.r;
     const int P = p.plen[r], tn = p.cnt[r], qbase = p.cu[r];
-    const int node = n0 + 8 * nsub + (c >> 2);
+    const int node = it.n0 + 8 * nsub + (c >> 2);
     const int qh = head * kGroups + (c & 3);
     const bool head_ok = head < p.num_kv_heads;
-    const bool wave_active = head_ok && (n0 + 8 * nsub) < tn;  // uniform per wave
+    const bool wave_active = head_ok && (it.n0 + 8 * nsub) < tn;  // uniform per wave
     const bool row_ok = head_ok && node < tn;
-    const int tree_end = (flags & 1) ? min(tn, n0 + npw) : 0;
-    const int ntp = (kend - kbeg + kTileKeys - 1) / kTileKeys;
+    const int tree_end = (it.flags & 1) ? min(tn, it.n0 + NPW) : 0;
+    const int ntp = (it.kend - it.kbeg + kTileKeys - 1) / kTileKeys;
     const int nt = ntp + (tree_end + kTileKeys - 1) / kTileKeys;
+    const int B = p.block_size;
+    const int64_t pool_slots = p.num_blocks * B;
+    const int page0 = it.kbeg / B;
+    const int npages = it.kend > it.kbeg ? (it.kend - 1) / B - page0 + 1 : 0;
+    // The planner keeps every item within the LDS page/slot caches and non-empty.
+    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots) {
+        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+        return;
+    }
+
+    // Page numbers of the prefix chunk and slots of the tree, validated, into LDS.
+    int32_t* pages = reinterpret_cast<int32_t*>(smem + kPagesOffset);
+    int32_t* tslots = reinterpret_cast<int32_t*>(smem + kSlotsOffset);
+    for (int i = tid; i < npages; i += kThreads) {
+        int32_t pg = p.tables[static_cast<int64_t>(r) * p.t_s0 + page0 + i];
+        if (pg < 0 || pg >= p.num_blocks) {
+            set_status(p.status, TV_STATUS_BAD_PAGE);
+            pg = 0;
+        }
+        pages[i] = pg;
+    }
+    for (int i = tid; i < tree_end; i += kThreads) {
+        int64_t s = p.tree_slots[qbase + i];
+        if (s < 0 || s >= pool_slots) {
+            set_status(p.status, TV_STATUS_BAD_PAGE);
+            s = 0;
+        }
+        tslots[i] = static_cast<int32_t>(s);
+    }
 
     // Q^T operand: lane (c, g) holds score row c, dims 16*st + 8*g + 0..7.
     V8 qb[8];
@@ -196,72 +213,63 @@ tree_attention_kernel(const AttnParams p) {
             qb[st] = __builtin_bit_cast(V8, raw);
         }
     }
+    __syncthreads();  // page and slot lists visible
 
-    // Staging assignment.  K: thread -> (key, 16-byte dim chunk), one per head.
-    // V: unit -> (key quad a, dim quad u, head); 4 keys x 4 dims per unit.
-    const int k_key = tid >> 4, k_chunk = tid & 15;
-    const int v_units = 256 * hpw;
+    // Staging: thread -> (key, 16-byte chunk) of K and of V, for each of the HPW heads.
+    const int s_key = tid >> 4, s_chunk = tid & 15;
     const T* kbase = static_cast<const T*>(p.k);
     const T* vbase = static_cast<const T*>(p.v);
-    u32x4 kreg[kMaxHpw];
-    u32x2 vreg[2][4];
+    u32x4 kst[PF][HPW];
+    u32x4 vst[PF][HPW];
+    uint32_t mst[PF];
 
-    auto gload = [&](int t) {
-        const KeyRow kr = key_row(p, r, qbase, kbeg, kend, ntp, tree_end, t, k_key);
-#pragma unroll
-        for (int j = 0; j < kMaxHpw; ++j) {
-            u32x4 x = {0u, 0u, 0u, 0u};
-            if (j < hpw && kr.valid && h0 + j < p.num_kv_heads) {
-                x = *reinterpret_cast<const u32x4*>(kbase + kr.k_off + static_cast<int64_t>(h0 + j) * p.k_s2 +
-                                                    8 * k_chunk);
-            }
-            kreg[j] = x;
+    // Row offsets (elements) of this thread's staging key in tile t.  Keys past the
+    // item's range read the tile's first key instead (finite data, masked later), so
+    // every load in the pipeline is unconditional and in bounds.
+    auto key_offsets = [&](int t, int64_t& koff, int64_t& voff) {
+        int64_t page, off;
+        if (t < ntp) {
+            int pos = it.kbeg + kTileKeys * t + s_key;
+            if (pos >= it.kend) pos = it.kbeg + kTileKeys * t;
+            page = pages[pos / B - page0];
+            off = pos % B;
+        } else {
+            int m = kTileKeys * (t - ntp) + s_key;
+            if (m >= tree_end) m = kTileKeys * (t - ntp);
+            const int64_t slot = tslots[m];
+            page = slot / B;
+            off = slot - page * B;
         }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int id = tid + kThreads * j;
-            const int a = id & 7, u = (id >> 3) & 31, vh = id >> 8;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                u32x2 x = {0u, 0u};
-                if (id < v_units && h0 + vh < p.num_kv_heads) {
-                    const KeyRow vr = key_row(p, r, qbase, kbeg, kend, ntp, tree_end, t, 4 * a + i);
-                    if (vr.valid) {
-                        x = *reinterpret_cast<const u32x2*>(vbase + vr.v_off + static_cast<int64_t>(h0 + vh) * p.v_s2 +
-                                                            4 * u);
-                    }
-                }
-                vreg[j][i] = x;
-            }
-        }
+        koff = page * p.k_s0 + off * p.k_s1;
+        voff = page * p.v_s0 + off * p.v_s1;
     };
 
-    auto sstore = [&](int stage) {
-        char* base = smem + stage * kStageBytes;
+    // Ancestor bits of this lane's node for tree tile t (read for every tile, used
+    // only for tree tiles; rows past the tree read node 0's word).
+    const uint32_t* anc_row = reinterpret_cast<const uint32_t*>(
+        p.anc + static_cast<int64_t>(qbase + (row_ok ? node : 0)) * p.words);
+
+    auto gload = [&](int t, u32x4 (&kd)[HPW], u32x4 (&vd)[HPW], uint32_t& md) {
+        int64_t koff, voff;
+        key_offsets(t, koff, voff);
 #pragma unroll
-        for (int j = 0; j < kMaxHpw; ++j) {
-            if (j < hpw) {
-                *reinterpret_cast<u32x4*>(base + j * kKHeadBytes + (k_key * kKRow + 8 * k_chunk) * 2) = kreg[j];
-            }
+        for (int j = 0; j < HPW; ++j) {
+            const int hh = min(it.h0 + j, p.num_kv_heads - 1);
+            kd[j] = *reinterpret_cast<const u32x4*>(kbase + koff + hh * p.k_s2 + 8 * s_chunk);
+            vd[j] = *reinterpret_cast<const u32x4*>(vbase + voff + hh * p.v_s2 + 8 * s_chunk);
         }
-        char* vt = base + hpw * kKHeadBytes;
+        const int m0 = t >= ntp ? kTileKeys * (t - ntp) : 0;
+        md = anc_row[m0 >> 5];
+    };
+
+    auto sstore = [&](int stage, const u32x4 (&kd)[HPW], const u32x4 (&vd)[HPW]) {
+        char* base = smem + stage * kStageBytes;
+        const int kpos = (s_chunk ^ k_swizzle(s_key)) * 16;
+        const int vpos = (s_chunk ^ v_swizzle(s_key)) * 16;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int id = tid + kThreads * j;
-            if (id < v_units) {
-                const int a = id & 7, u = (id >> 3) & 31, vh = id >> 8;
-                const int p0 = 16 * (a >> 2) + 8 * (a & 1) + 4 * ((a >> 1) & 1);
-                char* dst = vt + vh * kVHeadBytes + ((4 * u) * kVRow + p0) * 2;
-                const u32x2* k4 = vreg[j];
-                const u32x2 d0 = {pack_lo(k4[0].x, k4[1].x), pack_lo(k4[2].x, k4[3].x)};
-                const u32x2 d1 = {pack_hi(k4[0].x, k4[1].x), pack_hi(k4[2].x, k4[3].x)};
-                const u32x2 d2 = {pack_lo(k4[0].y, k4[1].y), pack_lo(k4[2].y, k4[3].y)};
-                const u32x2 d3 = {pack_hi(k4[0].y, k4[1].y), pack_hi(k4[2].y, k4[3].y)};
-                *reinterpret_cast<u32x2*>(dst + 0 * kVRow * 2) = d0;
-                *reinterpret_cast<u32x2*>(dst + 1 * kVRow * 2) = d1;
-                *reinterpret_cast<u32x2*>(dst + 2 * kVRow * 2) = d2;
-                *reinterpret_cast<u32x2*>(dst + 3 * kVRow * 2) = d3;
-            }
+        for (int j = 0; j < HPW; ++j) {
+            *reinterpret_cast<u32x4*>(base + (2 * j) * kTileBytes + s_key * kRowBytes + kpos) = kd[j];
+            *reinterpret_cast<u32x4*>(base + (2 * j + 1) * kTileBytes + s_key * kRowBytes + vpos) = vd[j];
         }
     };
 
@@ -271,45 +279,55 @@ tree_attention_kernel(const AttnParams p) {
     float m_run = -INFINITY, l_run = 0.f;
     const float cs = p.c;
 
-    auto compute = [&](int stage, int t) {
-        const char* kh = smem + stage * kStageBytes + hl * kKHeadBytes;
+    // Lane-constant parts of the operand addresses.
+    const int k_read = c * kRowBytes;                   // + ((2*st+g) ^ (c&7)) * 16
+    const int grp = lane >> 4, src = lane & 15;
+    const int v_key = 4 * (grp >> 1) + (src >> 2);      // + 16*kk + 8*h
+    const int v_chunk = 2 * (grp & 1) + ((src & 3) >> 1);  // + 4*db
+    const int v_half = (src & 1) * 8;
+
+    auto compute = [&](int stage, int t, uint32_t tree_bits) {
+        const char* kt = smem + stage * kStageBytes + (2 * hl) * kTileBytes;
+        const char* vt = kt + kTileBytes;
+        // LDS-typed view for the transposing reads (a C cast is the address-space cast).
+        __attribute__((address_space(3))) char* lds_vt = (__attribute__((address_space(3))) char*)(vt);
         f32x16 s = f32x16{};
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
-            const V8 a = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(kh + (c * kKRow + 16 * st + 8 * g) * 2));
+            const int pos = ((2 * st + g) ^ k_swizzle(c)) * 16;
+            const V8 a = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(kt + k_read + pos));
             s = Mfma<T>::run(a, qb[st], s);
         }
         // Visibility of the 16 keys this lane holds: key index 8*(v/4) + 4*g + v%4.
         if (t < ntp) {
-            const int nvalid = kend - (kbeg + kTileKeys * t);
+            const int nvalid = it.kend - (it.kbeg + kTileKeys * t);
             if (nvalid < kTileKeys) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const int key = 8 * (v >> 2) + 4 * g + (v & 3);
-                    if (key >= nvalid) s[v] = -INFINITY;
+                    if (8 * (v >> 2) + 4 * g + (v & 3) >= nvalid) s[v] = -INFINITY;
                 }
             }
         } else {
-            const int m0 = kTileKeys * (t - ntp);
-            uint32_t bits = 0;
-            if (row_ok) {
-                bits = static_cast<uint32_t>(p.anc[static_cast<int64_t>(qbase + node) * p.words + (m0 >> 6)] >>
-                                             (m0 & 32));
-            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int key = 8 * (v >> 2) + 4 * g + (v & 3);
-                if (!((bits >> key) & 1u)) s[v] = -INFINITY;
+                if (!((tree_bits >> (8 * (v >> 2) + 4 * g + (v & 3))) & 1u)) s[v] = -INFINITY;
             }
         }
         float mx = s[0];
 #pragma unroll
         for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float mc = m_use * cs;
-        const float alpha = __builtin_amdgcn_exp2f(m_run * cs - mc);
+        // Raise the reference maximum only when this tile would exceed it by 2^8.
+        const bool raise = mx * cs > m_run * cs + kRescaleThreshold;
+        if (__any(raise)) {
+            const float m_new = raise ? mx : m_run;
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * cs);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            m_run = m_new;
+        }
+        const float mc = (m_run == -INFINITY ? 0.f : m_run) * cs;
         float pr[16];
         float ps = 0.f;
 #pragma unroll
@@ -317,45 +335,51 @@ tree_attention_kernel(const AttnParams p) {
             pr[v] = __builtin_amdgcn_exp2f(fmaf(s[v], cs, -mc));
             ps += pr[v];
         }
-        ps += __shfl_xor(ps, 32);
-        l_run = l_run * alpha + ps;
-        m_run = m_new;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+        l_run += ps + __shfl_xor(ps, 32);
         V8 pb[2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
             for (int t8 = 0; t8 < 8; ++t8) pb[kk][t8] = static_cast<T>(pr[8 * kk + t8]);
         }
-        const char* vh = smem + stage * kStageBytes + hpw * kKHeadBytes + hl * kVHeadBytes;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                const V8 a = __builtin_bit_cast(
-                    V8, *reinterpret_cast<const u32x4*>(vh + ((32 * db + c) * kVRow + 16 * kk + 8 * g) * 2));
+            for (int db = 0; db < 4; ++db) {
+                i16x4 half[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int key = 16 * kk + 8 * h + v_key;
+                    const int off = key * kRowBytes + (((4 * db + v_chunk) ^ v_swizzle(key)) * 16) + v_half;
+                    half[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(lds_vt + off));
+                }
+                const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[db] = Mfma<T>::run(a, pb[kk], acc[db]);
             }
         }
     };
 
-    if (nt > 0) {
-        gload(0);
-        sstore(0);
-    }
-    if (nt > 1) gload(1);
-    __syncthreads();
-    for (int t = 0; t < nt; ++t) {
-        if (wave_active) compute(t & 1, t);
-        if (t + 1 < nt) sstore((t + 1) & 1);
-        if (t + 2 < nt) gload(t + 2);
-        __syncthreads();
+    // Prologue: the first PF tiles in flight (indices past the end repeat the last
+    // tile, so the pipeline never branches around a load).
+    const int last = nt - 1;
+#pragma unroll
+    for (int b = 0; b < PF; ++b) gload(min(b, last), kst[b], vst[b], mst[b]);
+    for (int t0 = 0; t0 < nt; t0 += PF) {
+#pragma unroll
+        for (int b = 0; b < PF; ++b) {
+            const int t = t0 + b;
+            const int stage = t & 1;
+            sstore(stage, kst[b], vst[b]);
+            const uint32_t bits = mst[b];
+            gload(min(t + PF, last), kst[b], vst[b], mst[b]);
+            __syncthreads();
+            if (t < nt && wave_active) compute(stage, t, bits);
+        }
     }
 
     if (!wave_active || !row_ok) return;
     const int wr = wave * 32 + c;  // score row within the item
-    if (slot < 0) {
+    if (it.slot < 0) {
         const float inv = 1.f / l_run;
         const int64_t row = qbase + node;
 #pragma unroll
@@ -368,7 +392,7 @@ tree_attention_kernel(const AttnParams p) {
             }
         }
     } else {
-        float* wo = p.ws_o + (static_cast<int64_t>(slot) * kRowsPerItem + wr) * kHeadDim;
+        float* wo = p.ws_o + (static_cast<int64_t>(it.slot) * kRowsPerItem + wr) * kHeadDim;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -377,7 +401,27 @@ tree_attention_kernel(const AttnParams p) {
                 *reinterpret_cast<f32x4*>(wo + 32 * db + 8 * i4 + 4 * g) = o;
             }
         }
-        if (g == 0) p.ws_ml[static_cast<int64_t>(slot) * kRowsPerItem + wr] = make_float2(m_run, l_run);
+        if (g == 0) p.ws_ml[static_cast<int64_t>(it.slot) * kRowsPerItem + wr] = make_float2(m_run, l_run);
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kThreads)
+tree_attention_kernel(const AttnParams p) {
+    __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+    const int32_t* d = p.items + 8 * blockIdx.x;
+    const Item it{d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7]};
+    if (it.r < 0 || it.r >= p.num_requests) {
+        if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+        return;
+    }
+    switch (it.hpw) {
+        case 1: run_item<T, 1>(p, smem, it); break;
+        case 2: run_item<T, 2>(p, smem, it); break;
+        case 4: run_item<T, 4>(p, smem, it); break;
+        default:
+            if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+            break;
     }
 }
 

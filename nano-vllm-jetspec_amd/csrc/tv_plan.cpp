@@ -24,6 +24,8 @@ constexpr int kItemInts = 8;
 constexpr int kRowsPerItem = 256;   // score rows of one workgroup
 constexpr int kHeadDim = 128;
 constexpr int kMinChunkKeys = 256;  // shortest prefix chunk worth a partial result
+constexpr int kMaxChunkPages = 512; // page numbers a workgroup caches in LDS
+constexpr int kMaxTreeNodes = 1024; // tree slots a workgroup caches in LDS
 
 struct Item {
     int32_t r, h0, n0, kbeg, kend, flags, slot, hpw;
@@ -65,6 +67,10 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         const int32_t p = prefix_lens_host[r], t = node_counts_host[r];
         if (p < 0) return fail(TV_ERR_INVALID, "plan: negative prefix length for request %d", r);
         if (t < 1) return fail(TV_ERR_INVALID, "plan: request %d has no tree nodes", r);
+        if (t > kMaxTreeNodes) {
+            return fail(TV_ERR_UNSUPPORTED, "plan: request %d has %d tree nodes (at most %d per request)", r, t,
+                        kMaxTreeNodes);
+        }
         max_nodes = std::max(max_nodes, t);
         const int hpw = heads_per_group(t, num_kv_heads);
         const int npw = 64 / hpw;
@@ -73,6 +79,11 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         total_cost += groups * blocks * hpw * (static_cast<int64_t>(p) + t);
     }
     const int64_t target = std::max<int64_t>(kMinChunkKeys, total_cost / num_compute_units);
+    // Longest chunk whose pages fit the LDS page cache wherever it starts.
+    const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
+    if (chunk_keys > max_chunk) {
+        return fail(TV_ERR_INVALID, "plan: chunk_keys %d exceeds %lld", chunk_keys, (long long)max_chunk);
+    }
 
     std::vector<Item> items;
     int32_t num_slots = 0, num_groups = 0;
@@ -86,7 +97,7 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         if (chunk_keys > 0) {
             chunk = chunk_keys;
         } else {
-            chunk = round_up(std::max<int64_t>(kMinChunkKeys, target / hpw), 32);
+            chunk = std::min(round_up(std::max<int64_t>(kMinChunkKeys, target / hpw), 32), max_chunk);
             const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
             chunk = round_up((p + nchunks - 1) / std::max<int64_t>(nchunks, 1), 32);
             if (chunk < 32) chunk = 32;

@@ -91,7 +91,7 @@ def test_commit_bit_exact_against_oracle(overlap):
     torch.cuda.synchronize()
     assert payload == 200 * 2 * 4 * 8 * 128 * 2
     assert oracle.copy_accepted_kv(expect, src, dst) == payload
-    assert np.array_equal(as_bytes(pool), expect.view(np.uint8).reshape(-1))
+    assert np.array_equal(as_bytes(pool).reshape(-1), expect.view(np.uint8).reshape(-1))
     assert read_and_clear_status(DEV) == 0
 
 
