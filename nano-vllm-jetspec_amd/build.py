@@ -39,6 +39,33 @@ def hipcc() -> str:
     return path
 
 
+def check_m0_discipline(verbose: bool = False) -> None:
+    """The attention kernel issues its global->LDS DMA from inline asm that sets M0.
+
+    That is only sound while no compiler-generated instruction of the kernel uses M0,
+    so compile the device code to assembly and require every M0 reference to be one
+    of those `s_mov_b32 m0, sN` writes.
+    """
+    import re
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as tmp:
+        asm = Path(tmp) / "tv_attention.s"
+        cmd = [hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-S", "--cuda-device-only",
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{REPO / 'include'}",
+               f"-I{CSRC}", str(CSRC / "tv_attention.hip"), "-o", str(asm)]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        if result.returncode != 0:
+            raise RuntimeError("hipcc -S failed:\n" + result.stderr)
+        bad = [line.strip() for line in asm.read_text().splitlines()
+               if re.search(r"\bm0\b", line) and not line.lstrip().startswith(";")
+               and not re.match(r"\s*s_mov_b32 m0, s\d+\s*$", line)]
+        if bad:
+            raise RuntimeError("compiler-generated M0 use would be clobbered by the DMA asm: " + "; ".join(bad[:5]))
+        if verbose:
+            print("M0 discipline ok", flush=True)
+
+
 def build(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
     tmp = OUTPUT.with_suffix(".so.tmp")
     cmd = [hipcc(), *HIP_FLAGS, *extra_flags, f"-I{REPO / 'include'}", f"-I{CSRC}",
@@ -55,6 +82,7 @@ def build(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
         raise RuntimeError("hipcc failed:\n" + "\n".join(messages))
     if verbose and messages:
         print("\n".join(messages), flush=True)
+    check_m0_discipline(verbose)
     os.replace(tmp, OUTPUT)
     return OUTPUT
 

@@ -17,7 +17,7 @@
 //                 depends on a load inside the loop: the chunk's page numbers and the
 //                 tree's slots are read into LDS once per work item.
 //   VGPR -> LDS   natural [key][dim] rows of 256 B with the 16-byte chunks XOR-
-//                 swizzled per key (K: chunk ^ key%8, V: chunk ^ 2*(key%4)), which
+//                 swizzled per key (K: chunk ^ key%16, V: chunk ^ 4*(key%4)), which
 //                 makes both operand reads below bank-conflict free.
 //   LDS -> MFMA   S^T[32 keys x 32 rows]  = K . Q^T   (8 x v_mfma_f32_32x32x16_bf16)
 //                 O^T[128 dims x 32 rows] += V^T . P^T (8 x v_mfma_f32_32x32x16_bf16)
@@ -54,6 +54,8 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -66,13 +68,14 @@ constexpr int kRowsPerItem = 256;
 constexpr int kTileKeys = 32;
 constexpr int kRowBytes = kHeadDim * 2;               // one K or V row of one head (bf16/f16)
 constexpr int kTileBytes = kTileKeys * kRowBytes;     // 8 KiB: K (or V) of one head, one tile
-constexpr int kMaxHpw = 4;
-constexpr int kStageBytes = kMaxHpw * 2 * kTileBytes; // 64 KiB: K and V of up to 4 heads
+constexpr int kMaskBytes = 8 * 64 * 4;                // per stage: each wave's 64 ancestor words
+// Tile stages: 8 of one head (HPW 1) or 4 of two heads (HPW 2); the larger is 144 KiB.
+constexpr int kRingBytes = 8 * (2 * kTileBytes + kMaskBytes);
 constexpr int kMaxPages = 512;                        // page numbers of one prefix chunk
 constexpr int kMaxTreeSlots = 1024;                   // tree slots cached per work item
-constexpr int kPagesOffset = 2 * kStageBytes;
+constexpr int kPagesOffset = kRingBytes;
 constexpr int kSlotsOffset = kPagesOffset + kMaxPages * 4;
-constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 137216 of gfx950's 160 KiB
+constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 153600 of gfx950's 160 KiB
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleThreshold = 8.f;              // log2 units
 
@@ -81,15 +84,26 @@ struct Mfma;
 template <>
 struct Mfma<__bf16> {
     typedef bf16x8_t vec;
+    typedef bf16x2_t pair;
     static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+    }
+    // acc + a.x + a.y in fp32 (one v_dot2 against (1, 1)).
+    static __device__ __forceinline__ float dot2(pair a, float acc) {
+        const pair one = {static_cast<__bf16>(1.f), static_cast<__bf16>(1.f)};
+        return __builtin_amdgcn_fdot2_f32_bf16(a, one, acc, false);
     }
 };
 template <>
 struct Mfma<_Float16> {
     typedef f16x8_t vec;
+    typedef f16x2_t pair;
     static __device__ __forceinline__ f32x16 run(vec a, vec b, f32x16 c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float dot2(pair a, float acc) {
+        const pair one = {static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
+        return __builtin_amdgcn_fdot2(a, one, acc, false);
     }
 };
 
@@ -123,8 +137,12 @@ struct AttnParams {
     int32_t* status;
 };
 
-__device__ __forceinline__ int k_swizzle(int key) { return key & 7; }
-__device__ __forceinline__ int v_swizzle(int key) { return 2 * (key & 3); }
+// gfx950 LDS serves 256 B per clock from 64 banks.  K operand reads (ds_read_b128,
+// 16 keys at one chunk per clock) need 16 distinct chunk positions; the transposing V
+// reads (4 keys x 4 chunks per clock) need 4 keys spread by multiples of 4 chunks.
+// Both swizzles measured 0 bank conflicts with SQ_LDS_BANK_CONFLICT.
+__device__ __forceinline__ int k_swizzle(int key) { return key & 15; }
+__device__ __forceinline__ int v_swizzle(int key) { return 4 * (key & 3); }
 
 template <typename T>
 __device__ __forceinline__ void store_out4(const AttnParams& p, int64_t row, int qh, int dim, f32x4 v) {
@@ -145,28 +163,83 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
+// Global -> LDS DMA of 16 (or 4) bytes per lane into LDS at `lds_addr` + 16 * lane
+// (+ 4 * lane).  Issued from inline asm so the compiler's wait-count pass does not
+// treat every later LDS read as dependent on the DMA (it would wait for vmcnt(0));
+// the kernel orders the DMA explicitly with wait_vmcnt + a workgroup barrier.
+// M0 is otherwise unused by this kernel (no LDS DMA builtins, GWS or indexed VGPR
+// moves are emitted), so clobbering it here is safe; the kernel's ISA is checked for
+// other M0 writes when it is built (nano-vllm-jetspec_amd/build.py).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_b128(const void* src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds_addr), "v"(src)
+                 : "memory", "m0");
+}
+// Scalar-base forms: address = 64-bit SGPR base + 32-bit per-lane VGPR byte offset.
+__device__ __forceinline__ void dma_b128_s(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(lds_addr), "v"(lane_offset), "s"(base)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b32_s(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
+                 :
+                 : "s"(lds_addr), "v"(lane_offset), "s"(base)
+                 : "memory", "m0");
+}
+
+#pragma clang diagnostic pop
+
 struct Item {
     int r, h0, n0, kbeg, kend, flags, slot, hpw;
 };
+
+// A pointer the caller knows to be wave-uniform, moved to SGPRs.
+__device__ __forceinline__ const void* uniform_ptr(const void* ptr) {
+    const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Keeps the compiler from moving instructions across this point, so the hand-made
+// MFMA / LDS / VALU interleave of the tile step survives scheduling.
+__device__ __forceinline__ void order_point() { __builtin_amdgcn_sched_barrier(0); }
 
 // One work item with HPW KV heads per workgroup.
 template <typename T, int HPW>
 __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it) {
     typedef typename Mfma<T>::vec V8;
-    constexpr int PF = 4 / HPW;   // tiles of K/V in flight per thread
-    constexpr int WPH = 8 / HPW;  // waves per KV head
-    constexpr int NPW = 8 * WPH;  // nodes per workgroup
+    typedef typename Mfma<T>::pair V2;
+    typedef __attribute__((address_space(3))) char lds_char;
+    constexpr int WPH = 8 / HPW;                        // waves per KV head
+    constexpr int NPW = 8 * WPH;                        // nodes per workgroup
+    // LDS ring of NS stages.  K tiles, V tiles and ancestor words live in three regions
+    // so every operand address is a per-lane constant plus a compile-time stage offset.
+    constexpr int NS = HPW == 1 ? 8 : 4;
+    constexpr int TILE_SET = HPW * kTileBytes;          // K (or V) of the HPW heads, one stage
+    constexpr int V_REGION = NS * TILE_SET;
+    constexpr int M_REGION = 2 * NS * TILE_SET;
+    constexpr int LPT = 2 * HPW + 1;                    // DMA loads per tile per wave
+    static_assert(M_REGION + NS * kMaskBytes <= kRingBytes, "ring exceeds its LDS region");
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+    // `wave` is the same in all lanes; readfirstlane lets the compiler see that, so
+    // every per-wave quantity below lives in SGPRs and per-wave branches are scalar.
+    const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, g = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hl = wave / WPH;
     const int head = it.h0 + hl;
     const int nsub = wave - hl * WPH;
     const int r = it.r;
-    const int P = p.plen[r], tn = p.cnt[r], qbase = p.cu[r];
+    const int tn = p.cnt[r], qbase = p.cu[r];
     const int node = it.n0 + 8 * nsub + (c >> 2);
     const int qh = head * kGroups + (c & 3);
     const bool head_ok = head < p.num_kv_heads;
-    const bool wave_active = head_ok && (it.n0 + 8 * nsub) < tn;  // uniform per wave
+    const bool wave_active = head_ok && (it.n0 + 8 * nsub) < tn;
     const bool row_ok = head_ok && node < tn;
     const int tree_end = (it.flags & 1) ? min(tn, it.n0 + NPW) : 0;
     const int ntp = (it.kend - it.kbeg + kTileKeys - 1) / kTileKeys;
@@ -193,12 +266,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         pages[i] = pg;
     }
     for (int i = tid; i < tree_end; i += kThreads) {
-        int64_t s = p.tree_slots[qbase + i];
-        if (s < 0 || s >= pool_slots) {
+        int64_t sl = p.tree_slots[qbase + i];
+        if (sl < 0 || sl >= pool_slots) {
             set_status(p.status, TV_STATUS_BAD_PAGE);
-            s = 0;
+            sl = 0;
         }
-        tslots[i] = static_cast<int32_t>(s);
+        tslots[i] = static_cast<int32_t>(sl);
     }
 
     // Q^T operand: lane (c, g) holds score row c, dims 16*st + 8*g + 0..7.
@@ -213,171 +286,259 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             qb[st] = __builtin_bit_cast(V8, raw);
         }
     }
+    // Retire the Q loads here: the tile loop then contains no compiler-tracked vector
+    // load, so the only vmcnt waits in it are the explicit per-tile ones below.
+    wait_vmcnt<0>();
     __syncthreads();  // page and slot lists visible
 
-    // Staging: thread -> (key, 16-byte chunk) of K and of V, for each of the HPW heads.
-    const int s_key = tid >> 4, s_chunk = tid & 15;
-    const T* kbase = static_cast<const T*>(p.k);
-    const T* vbase = static_cast<const T*>(p.v);
-    u32x4 kst[PF][HPW];
-    u32x4 vst[PF][HPW];
-    uint32_t mst[PF];
+    lds_char* lds = (lds_char*)(smem);
+    // Per-lane LDS operand offsets (stage 0).
+    //   K, MFMA step st: key c, chunk 2*st+g at position (2*st+g) ^ (c%16).
+    //   V, output block db: key vk (+16*kk+8*h), chunk 4*db+vc at position ^ 4*(vk%4).
+    uint32_t k_ofs[8];
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+        k_ofs[st] = hl * kTileBytes + c * kRowBytes + (((2 * st + g) ^ k_swizzle(c)) & 15) * 16;
+    }
+    const int grp = lane >> 4, src = lane & 15;
+    const int vk = 4 * (grp >> 1) + (src >> 2);
+    const int vc = 2 * (grp & 1) + ((src & 3) >> 1);
+    uint32_t v_ofs[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+        v_ofs[db] = V_REGION + hl * kTileBytes + vk * kRowBytes + (((4 * db + vc) ^ v_swizzle(vk)) & 15) * 16 +
+                    (src & 1) * 8;
+    }
+    const uint32_t m_ofs = M_REGION + wave * 256 + 4 * (c >> 2);
 
-    // Row offsets (elements) of this thread's staging key in tile t.  Keys past the
-    // item's range read the tile's first key instead (finite data, masked later), so
-    // every load in the pipeline is unconditional and in bounds.
-    auto key_offsets = [&](int t, int64_t& koff, int64_t& voff) {
-        int64_t page, off;
-        if (t < ntp) {
-            int pos = it.kbeg + kTileKeys * t + s_key;
-            if (pos >= it.kend) pos = it.kbeg + kTileKeys * t;
-            page = pages[pos / B - page0];
-            off = pos % B;
+    // Staging: global -> LDS DMA (global_load_lds_dwordx4 writes lane L's 16 bytes at
+    // the wave's LDS base + 16*L).  Wave w moves keys 4w..4w+3 of every tile: lane L
+    // loads key 4w + L/16 and the 16-byte chunk that belongs at LDS position L%16 of
+    // that key's row, i.e. global chunk (L%16) ^ swizzle(key).  Prefix tiles address
+    // a scalar page base plus these per-lane byte offsets (host-checked to fit 31 bits).
+    const int s_key = tid >> 4;
+    const int k_chunk = (lane & 15) ^ k_swizzle(s_key);
+    const int v_chunk = (lane & 15) ^ v_swizzle(s_key);
+    const uint32_t k_chunk_b = 16u * k_chunk, v_chunk_b = 16u * v_chunk;
+    const uint32_t k_lane_b = static_cast<uint32_t>(s_key * p.k_s1 * static_cast<int64_t>(sizeof(T))) + k_chunk_b;
+    const uint32_t v_lane_b = static_cast<uint32_t>(s_key * p.v_s1 * static_cast<int64_t>(sizeof(T))) + v_chunk_b;
+    const T* kh[HPW];
+    const T* vh[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+        const int64_t hh = min(it.h0 + j, p.num_kv_heads - 1);
+        kh[j] = static_cast<const T*>(p.k) + hh * p.k_s2;
+        vh[j] = static_cast<const T*>(p.v) + hh * p.v_s2;
+    }
+    const bool pow2 = (B & (B - 1)) == 0;
+    const int bshift = __builtin_ctz(B);
+
+    // Ancestor bits: lane L of wave w fetches the word of node n0 + 8*nsub + L%8 (the
+    // wave's own 8 nodes; rows past the tree read the last node's word).
+    const int mask_node = min(it.n0 + 8 * nsub + (lane & 7), tn - 1);
+    const uint32_t m_lane_b = static_cast<uint32_t>(mask_node * p.words * 8);
+    const char* anc_req = reinterpret_cast<const char*>(p.anc + static_cast<int64_t>(qbase) * p.words);
+
+    // Enqueues tile t into `stage`.  Keys past the item's range, and tiles past the
+    // last one, read the tile's first key (finite data, masked later; cache hits), so
+    // every wave issues exactly LPT loads per tile and every load is in bounds.
+    auto issue = [&](int t, int stage) {
+        const int tt = t < nt ? t : nt - 1;
+        const uint32_t kdst = __builtin_amdgcn_readfirstlane(
+            static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds + stage * TILE_SET + wave * 1024)));
+        const uint32_t mdst = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
+            reinterpret_cast<uintptr_t>(lds + M_REGION + stage * kMaskBytes + wave * 256)));
+        if (tt < ntp) {
+            // Page and first offset of the tile are wave-uniform: scalar arithmetic.
+            const uint32_t tile_pos = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it.kbeg + kTileKeys * tt));
+            const uint32_t page_abs = pow2 ? (tile_pos >> bshift) : (tile_pos / static_cast<uint32_t>(B));
+            const int64_t page = __builtin_amdgcn_readfirstlane(pages[page_abs - page0]);
+            const int64_t off0 = tile_pos - page_abs * static_cast<uint32_t>(B);
+            const int64_t kt = page * p.k_s0 + off0 * p.k_s1;
+            const int64_t vt = page * p.v_s0 + off0 * p.v_s1;
+            uint32_t kl = k_lane_b, vl = v_lane_b;
+            if (static_cast<int>(tile_pos) + kTileKeys > it.kend) {
+                const bool in = static_cast<int>(tile_pos) + s_key < it.kend;
+                kl = in ? kl : k_chunk_b;
+                vl = in ? vl : v_chunk_b;
+            }
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) {
+                dma_b128_s(kl, uniform_ptr(kh[j] + kt), kdst + j * kTileBytes);
+                dma_b128_s(vl, uniform_ptr(vh[j] + vt), kdst + V_REGION + j * kTileBytes);
+            }
+            dma_b32_s(m_lane_b, uniform_ptr(anc_req), mdst);
         } else {
-            int m = kTileKeys * (t - ntp) + s_key;
-            if (m >= tree_end) m = kTileKeys * (t - ntp);
-            const int64_t slot = tslots[m];
-            page = slot / B;
-            off = slot - page * B;
-        }
-        koff = page * p.k_s0 + off * p.k_s1;
-        voff = page * p.v_s0 + off * p.v_s1;
-    };
-
-    // Ancestor bits of this lane's node for tree tile t (read for every tile, used
-    // only for tree tiles; rows past the tree read node 0's word).
-    const uint32_t* anc_row = reinterpret_cast<const uint32_t*>(
-        p.anc + static_cast<int64_t>(qbase + (row_ok ? node : 0)) * p.words);
-
-    auto gload = [&](int t, u32x4 (&kd)[HPW], u32x4 (&vd)[HPW], uint32_t& md) {
-        int64_t koff, voff;
-        key_offsets(t, koff, voff);
+            const int m0 = kTileKeys * (tt - ntp);
+            int m = m0 + s_key;
+            if (m >= tree_end) m = m0;
+            const int slot = tslots[m];
+            const int pg = pow2 ? (slot >> bshift) : (slot / B);
+            const int off = slot - pg * B;
+            const int64_t koff = static_cast<int64_t>(pg) * p.k_s0 + static_cast<int64_t>(off) * p.k_s1 + 8 * k_chunk;
+            const int64_t voff = static_cast<int64_t>(pg) * p.v_s0 + static_cast<int64_t>(off) * p.v_s1 + 8 * v_chunk;
 #pragma unroll
-        for (int j = 0; j < HPW; ++j) {
-            const int hh = min(it.h0 + j, p.num_kv_heads - 1);
-            kd[j] = *reinterpret_cast<const u32x4*>(kbase + koff + hh * p.k_s2 + 8 * s_chunk);
-            vd[j] = *reinterpret_cast<const u32x4*>(vbase + voff + hh * p.v_s2 + 8 * s_chunk);
-        }
-        const int m0 = t >= ntp ? kTileKeys * (t - ntp) : 0;
-        md = anc_row[m0 >> 5];
-    };
-
-    auto sstore = [&](int stage, const u32x4 (&kd)[HPW], const u32x4 (&vd)[HPW]) {
-        char* base = smem + stage * kStageBytes;
-        const int kpos = (s_chunk ^ k_swizzle(s_key)) * 16;
-        const int vpos = (s_chunk ^ v_swizzle(s_key)) * 16;
-#pragma unroll
-        for (int j = 0; j < HPW; ++j) {
-            *reinterpret_cast<u32x4*>(base + (2 * j) * kTileBytes + s_key * kRowBytes + kpos) = kd[j];
-            *reinterpret_cast<u32x4*>(base + (2 * j + 1) * kTileBytes + s_key * kRowBytes + vpos) = vd[j];
+            for (int j = 0; j < HPW; ++j) {
+                dma_b128(kh[j] + koff, kdst + j * kTileBytes);
+                dma_b128(vh[j] + voff, kdst + V_REGION + j * kTileBytes);
+            }
+            dma_b32_s(m_lane_b, uniform_ptr(anc_req + (m0 >> 5) * 4), mdst);
         }
     };
 
     f32x16 acc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
-    float m_run = -INFINITY, l_run = 0.f;
+    // Per row: reference maximum m_run (score units), its exp2-domain threshold and
+    // offset, and this lane's half of the running sum.
+    float m_run = -INFINITY, thr = -INFINITY, nmc = 0.f, l_run = 0.f;
     const float cs = p.c;
+    // Tiles [0, nfull) are whole prefix tiles that need no mask.
+    const int nfull = (it.kend - it.kbeg) / kTileKeys;
 
-    // Lane-constant parts of the operand addresses.
-    const int k_read = c * kRowBytes;                   // + ((2*st+g) ^ (c&7)) * 16
-    const int grp = lane >> 4, src = lane & 15;
-    const int v_key = 4 * (grp >> 1) + (src >> 2);      // + 16*kk + 8*h
-    const int v_chunk = 2 * (grp & 1) + ((src & 3) >> 1);  // + 4*db
-    const int v_half = (src & 1) * 8;
-
-    auto compute = [&](int stage, int t, uint32_t tree_bits) {
-        const char* kt = smem + stage * kStageBytes + (2 * hl) * kTileBytes;
-        const char* vt = kt + kTileBytes;
-        // LDS-typed view for the transposing reads (a C cast is the address-space cast).
-        __attribute__((address_space(3))) char* lds_vt = (__attribute__((address_space(3))) char*)(vt);
-        f32x16 s = f32x16{};
-#pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const int pos = ((2 * st + g) ^ k_swizzle(c)) * 16;
-            const V8 a = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(kt + k_read + pos));
-            s = Mfma<T>::run(a, qb[st], s);
-        }
-        // Visibility of the 16 keys this lane holds: key index 8*(v/4) + 4*g + v%4.
-        if (t < ntp) {
-            const int nvalid = it.kend - (it.kbeg + kTileKeys * t);
-            if (nvalid < kTileKeys) {
+    // Masks tile tt's scores in place, then raises the reference maximum when the
+    // tile exceeds it by 2^8 (rescaling O and the sum, which then hold every earlier
+    // tile).  The decision and the new maximum are taken on the full row (both lane
+    // halves), so the halves of a row always share one reference.
+    auto prepare = [&](f32x16& s, int stage, int tt) {
+        if (tt >= nfull) {
+            // Visibility of the 16 keys this lane holds: key index 8*(v/4) + 4*g + v%4.
+            if (tt < ntp) {
+                const int nvalid = it.kend - (it.kbeg + kTileKeys * tt);
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     if (8 * (v >> 2) + 4 * g + (v & 3) >= nvalid) s[v] = -INFINITY;
                 }
-            }
-        } else {
+            } else {
+                const uint32_t tree_bits =
+                    row_ok ? *(const __attribute__((address_space(3))) uint32_t*)(lds + m_ofs + stage * kMaskBytes)
+                           : 0u;
+                const uint32_t half_bits = tree_bits >> (4 * g);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                if (!((tree_bits >> (8 * (v >> 2) + 4 * g + (v & 3))) & 1u)) s[v] = -INFINITY;
-            }
-        }
-        float mx = s[0];
-#pragma unroll
-        for (int v = 1; v < 16; ++v) mx = fmaxf(mx, s[v]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // Raise the reference maximum only when this tile would exceed it by 2^8.
-        const bool raise = mx * cs > m_run * cs + kRescaleThreshold;
-        if (__any(raise)) {
-            const float m_new = raise ? mx : m_run;
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * cs);
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-            m_run = m_new;
-        }
-        const float mc = (m_run == -INFINITY ? 0.f : m_run) * cs;
-        float pr[16];
-        float ps = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            pr[v] = __builtin_amdgcn_exp2f(fmaf(s[v], cs, -mc));
-            ps += pr[v];
-        }
-        l_run += ps + __shfl_xor(ps, 32);
-        V8 pb[2];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-            for (int t8 = 0; t8 < 8; ++t8) pb[kk][t8] = static_cast<T>(pr[8 * kk + t8]);
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                i16x4 half[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int key = 16 * kk + 8 * h + v_key;
-                    const int off = key * kRowBytes + (((4 * db + v_chunk) ^ v_swizzle(key)) * 16) + v_half;
-                    half[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(lds_vt + off));
+                for (int v = 0; v < 16; ++v) {
+                    if (!((half_bits >> (8 * (v >> 2) + (v & 3))) & 1u)) s[v] = -INFINITY;
                 }
-                const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(half[0], half[1], 0, 1, 2, 3, 4, 5, 6, 7));
-                acc[db] = Mfma<T>::run(a, pb[kk], acc[db]);
+            }
+        }
+        float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+        for (int v = 3; v < 15; v += 2) mx = fmaxf(fmaxf(mx, s[v]), s[v + 1]);
+        mx = fmaxf(mx, s[15]);
+        if (__any(mx * cs > thr)) {
+            const float row_max = fmaxf(mx, __shfl_xor(mx, 32));
+            if (row_max * cs > thr) {
+                const float alpha = __builtin_amdgcn_exp2f((m_run - row_max) * cs);
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+                m_run = row_max;
+                thr = row_max * cs + kRescaleThreshold;
+                nmc = -row_max * cs;
             }
         }
     };
 
-    // Prologue: the first PF tiles in flight (indices past the end repeat the last
-    // tile, so the pipeline never branches around a load).
-    const int last = nt - 1;
+    // One tile step, in a fixed issue order: the 8 QK^T MFMAs of tile t+1 and the 8
+    // P.V MFMAs of tile t alternate with the softmax VALU work of tile t (exp2, bf16
+    // packing, row sums), and every LDS operand is read two MFMA slots ahead of its
+    // use.  Each wave thus keeps its matrix core and its VALU busy at once instead of
+    // running the two phases back to back.
+    auto step = [&](const f32x16& s, f32x16& sn, const int kst, const int vst) {
+        V8 ka[8];
+        i16x4 vlo[8], vhi[8];
+        float pr[16];
+        V8 pb[2];
+        float l0 = 0.f, l1 = 0.f;
+        auto kread = [&](int i) {
+            ka[i] = __builtin_bit_cast(V8, *(const __attribute__((address_space(3))) u32x4*)(lds + k_ofs[i] + kst));
+        };
+        auto vread = [&](int kk, int db) {
+            vlo[4 * kk + db] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * kRowBytes));
+            vhi[4 * kk + db] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * kRowBytes));
+        };
+        auto qk_mfma = [&](int i) { sn = Mfma<T>::run(ka[i], qb[i], i == 0 ? f32x16{} : sn); };
+        auto pv_mfma = [&](int kk, int db) {
+            const V8 a = __builtin_bit_cast(
+                V8, __builtin_shufflevector(vlo[4 * kk + db], vhi[4 * kk + db], 0, 1, 2, 3, 4, 5, 6, 7));
+            acc[db] = Mfma<T>::run(a, pb[kk], acc[db]);
+        };
+        auto ex = [&](int e) { pr[e] = __builtin_amdgcn_exp2f(fmaf(s[e], cs, nmc)); };
+        auto pack = [&](int kk) {
 #pragma unroll
-    for (int b = 0; b < PF; ++b) gload(min(b, last), kst[b], vst[b], mst[b]);
-    for (int t0 = 0; t0 < nt; t0 += PF) {
+            for (int t8 = 0; t8 < 8; ++t8) pb[kk][t8] = static_cast<T>(pr[8 * kk + t8]);
+        };
+        // Row sums from the packed probabilities (the values the P.V product uses).
+        auto rsum = [&](int kk, float& l) {
 #pragma unroll
-        for (int b = 0; b < PF; ++b) {
+            for (int q2 = 0; q2 < 4; ++q2) {
+                const V2 two = {pb[kk][2 * q2], pb[kk][2 * q2 + 1]};
+                l = Mfma<T>::dot2(two, l);
+            }
+        };
+        kread(0);
+        kread(1);
+        order_point();
+        qk_mfma(0); kread(2); ex(0); ex(1); order_point();
+        qk_mfma(1); kread(3); ex(2); ex(3); order_point();
+        qk_mfma(2); kread(4); ex(4); ex(5); order_point();
+        qk_mfma(3); vread(0, 0); ex(6); ex(7); order_point();
+        qk_mfma(4); kread(5); pack(0); ex(8); ex(9); order_point();
+        pv_mfma(0, 0); vread(0, 1); ex(10); ex(11); order_point();
+        qk_mfma(5); kread(6); ex(12); ex(13); order_point();
+        pv_mfma(0, 1); vread(0, 2); ex(14); ex(15); rsum(0, l0); order_point();
+        qk_mfma(6); kread(7); pack(1); order_point();
+        pv_mfma(0, 2); vread(0, 3); rsum(1, l1); order_point();
+        qk_mfma(7); vread(1, 0); order_point();
+        pv_mfma(0, 3); vread(1, 1); order_point();
+        pv_mfma(1, 0); vread(1, 2); order_point();
+        pv_mfma(1, 1); vread(1, 3); order_point();
+        pv_mfma(1, 2); order_point();
+        pv_mfma(1, 3); order_point();
+        l_run += l0 + l1;
+    };
+
+    // Software pipeline over the tiles.  Prologue: tiles 0..NS-2 in flight, scores of
+    // tile 0.  Iteration t: wait for tile t+1 and barrier (publishes every wave's DMA
+    // of tile t+1 and retires stage (t-1)%NS, last read in iteration t-1), enqueue
+    // tile t+NS-1 into that stage, run the tile step (S of tile t+1, softmax and P.V
+    // of tile t), then mask tile t+1 and update the reference maximum.  The loop is
+    // unrolled NS times so every stage offset is a compile-time constant.
+#pragma unroll
+    for (int b = 0; b < NS - 1; ++b) issue(b, b);
+    wait_vmcnt<(NS - 2) * LPT>();
+    __syncthreads();
+    f32x16 s = f32x16{};
+    if (wave_active) {
+#pragma unroll
+        for (int st = 0; st < 8; ++st) {
+            const V8 a = __builtin_bit_cast(V8, *(const __attribute__((address_space(3))) u32x4*)(lds + k_ofs[st]));
+            s = Mfma<T>::run(a, qb[st], s);
+        }
+        prepare(s, 0, 0);
+    }
+    for (int t0 = 0; t0 < nt; t0 += NS) {
+#pragma unroll
+        for (int b = 0; b < NS; ++b) {
             const int t = t0 + b;
-            const int stage = t & 1;
-            sstore(stage, kst[b], vst[b]);
-            const uint32_t bits = mst[b];
-            gload(min(t + PF, last), kst[b], vst[b], mst[b]);
+            if (t >= nt) break;
+            wait_vmcnt<(NS - 3) * LPT>();
             __syncthreads();
-            if (t < nt && wave_active) compute(stage, t, bits);
+            issue(t + NS - 1, (b + NS - 1) % NS);
+            if (wave_active) {
+                f32x16 sn;
+                step(s, sn, ((b + 1) % NS) * TILE_SET, b * TILE_SET);
+                if (t + 1 < nt) prepare(sn, (b + 1) % NS, t + 1);
+                s = sn;
+            }
         }
     }
+    wait_vmcnt<0>();  // retire the padding loads before the workgroup ends
 
-    if (!wave_active || !row_ok) return;
+    if (!wave_active) return;
+    l_run += __shfl_xor(l_run, 32);  // both halves of the row
+    if (!row_ok) return;
     const int wr = wave * 32 + c;  // score row within the item
     if (it.slot < 0) {
         const float inv = 1.f / l_run;
@@ -418,7 +579,6 @@ tree_attention_kernel(const AttnParams p) {
     switch (it.hpw) {
         case 1: run_item<T, 1>(p, smem, it); break;
         case 2: run_item<T, 2>(p, smem, it); break;
-        case 4: run_item<T, 4>(p, smem, it); break;
         default:
             if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
             break;
@@ -540,6 +700,15 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
     if ((ks[0] | ks[1] | ks[2] | vs[0] | vs[1] | vs[2]) % 8 || (a->q_stride_row | a->q_stride_head) % 8 ||
         !aligned(a->q, 16) || !aligned(a->k_pool, 16) || !aligned(a->v_pool, 16)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: Q/K/V rows must be 16-byte aligned");
+    }
+    // Prefix tiles are fetched as page base + per-lane byte offset of up to 31 key rows.
+    if (ks[1] < 0 || vs[1] < 0 || ks[1] * 2 * kTileKeys >= (int64_t{1} << 31) ||
+        vs[1] * 2 * kTileKeys >= (int64_t{1} << 31)) {
+        return fail(TV_ERR_UNSUPPORTED, "tree_attention: K/V slot stride out of range");
+    }
+    if (a->ancestor_words_per_row < 1 || a->ancestor_words_per_row > kMaxTreeSlots / 64) {
+        return fail(TV_ERR_INVALID, "tree_attention: ancestor_words_per_row %d out of range",
+                    a->ancestor_words_per_row);
     }
     const int out_elem = a->out_dtype == TV_F32 ? 4 : 2;
     if ((a->out_stride_row | a->out_stride_head) % (16 / out_elem) || !aligned(a->out, 16)) {

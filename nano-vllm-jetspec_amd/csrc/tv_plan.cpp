@@ -4,7 +4,7 @@
 // (paged_backend.py:290) or per (4-node block, KV head) (tree_gqa.py:130), and every
 // program walks its request's whole prefix.  On MI355X the kernel instead gives a
 // 512-thread workgroup 256 score rows that share one K/V stream:
-//   HPW (KV heads per workgroup) = 4 / 2 / 1 for trees of <=16 / <=32 / >32 nodes,
+//   HPW (KV heads per workgroup) = 2 / 1 for trees of <=32 / >32 nodes,
 //   NPW (nodes per workgroup)    = 64 / HPW,
 // so a KV tile staged in LDS is reused by every (node, query head) row of its group.
 // Long prefixes are cut into chunks (split-K) only as far as needed to give every
@@ -34,7 +34,7 @@ struct Item {
 };
 
 int heads_per_group(int32_t nodes, int32_t kv_heads) {
-    int h = nodes <= 16 ? 4 : (nodes <= 32 ? 2 : 1);
+    int h = nodes <= 32 ? 2 : 1;
     while (h > 1 && h > kv_heads) h >>= 1;
     return h;
 }

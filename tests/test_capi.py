@@ -58,7 +58,7 @@ def test_entry_points_reject_bad_arguments_without_a_device():
 
 
 def heads_per_group(nodes, kv_heads):
-    h = 4 if nodes <= 16 else (2 if nodes <= 32 else 1)
+    h = 2 if nodes <= 32 else 1
     while h > 1 and h > kv_heads:
         h //= 2
     return h
