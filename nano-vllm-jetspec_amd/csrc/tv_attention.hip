@@ -77,7 +77,7 @@ constexpr int kPagesOffset = kRingBytes;
 constexpr int kSlotsOffset = kPagesOffset + kMaxPages * 4;
 constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 153600 of gfx950's 160 KiB
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kRescaleThreshold = 8.f;              // log2 units
+constexpr float kMaxTileSum = 256.f;                  // per lane half, against the reference
 
 template <typename T>
 struct Mfma;
@@ -210,6 +210,11 @@ __device__ __forceinline__ const void* uniform_ptr(const void* ptr) {
 // MFMA / LDS / VALU interleave of the tile step survives scheduling.
 __device__ __forceinline__ void order_point() { __builtin_amdgcn_sched_barrier(0); }
 
+// An empty use of a VGPR value: emits nothing, but keeps the computation of `x` in
+// the basic block where it is written, so code sinking cannot move VALU work out of
+// its slot (the tile step has a branchy scalar section in its middle).
+__device__ __forceinline__ void pin(float x) { asm volatile("" : : "v"(x)); }
+
 // One work item with HPW KV heads per workgroup.
 template <typename T, int HPW>
 __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it) {
@@ -224,7 +229,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     constexpr int TILE_SET = HPW * kTileBytes;          // K (or V) of the HPW heads, one stage
     constexpr int V_REGION = NS * TILE_SET;
     constexpr int M_REGION = 2 * NS * TILE_SET;
-    constexpr int LPT = 2 * HPW + 1;                    // DMA loads per tile per wave
+    constexpr int LPT = 2 * HPW;                        // DMA loads per tile per wave, at least
     static_assert(M_REGION + NS * kMaskBytes <= kRingBytes, "ring exceeds its LDS region");
 
     // `wave` is the same in all lanes; readfirstlane lets the compiler see that, so
@@ -314,21 +319,30 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // Staging: global -> LDS DMA (global_load_lds_dwordx4 writes lane L's 16 bytes at
     // the wave's LDS base + 16*L).  Wave w moves keys 4w..4w+3 of every tile: lane L
     // loads key 4w + L/16 and the 16-byte chunk that belongs at LDS position L%16 of
-    // that key's row, i.e. global chunk (L%16) ^ swizzle(key).  Prefix tiles address
-    // a scalar page base plus these per-lane byte offsets (host-checked to fit 31 bits).
+    // that key's row, i.e. global chunk (L%16) ^ swizzle(key).  Every load takes a
+    // per-lane 64-bit address: for a prefix tile the tile's page base (scalar
+    // arithmetic) plus a per-lane byte offset, for a tree tile the lane's own slot.
     const int s_key = tid >> 4;
     const int k_chunk = (lane & 15) ^ k_swizzle(s_key);
     const int v_chunk = (lane & 15) ^ v_swizzle(s_key);
     const uint32_t k_chunk_b = 16u * k_chunk, v_chunk_b = 16u * v_chunk;
-    const uint32_t k_lane_b = static_cast<uint32_t>(s_key * p.k_s1 * static_cast<int64_t>(sizeof(T))) + k_chunk_b;
-    const uint32_t v_lane_b = static_cast<uint32_t>(s_key * p.v_s1 * static_cast<int64_t>(sizeof(T))) + v_chunk_b;
-    const T* kh[HPW];
-    const T* vh[HPW];
+    // Byte strides; the host checks that a page stride fits 32 bits and 32 key rows 31.
+    const uint32_t k_page_b = static_cast<uint32_t>(p.k_s0 * static_cast<int64_t>(sizeof(T)));
+    const uint32_t v_page_b = static_cast<uint32_t>(p.v_s0 * static_cast<int64_t>(sizeof(T)));
+    const uint32_t k_key_b = static_cast<uint32_t>(p.k_s1 * static_cast<int64_t>(sizeof(T)));
+    const uint32_t v_key_b = static_cast<uint32_t>(p.v_s1 * static_cast<int64_t>(sizeof(T)));
+    const uint32_t k_lane_b = s_key * k_key_b + k_chunk_b;
+    const uint32_t v_lane_b = s_key * v_key_b + v_chunk_b;
+    // Head h0 of the group, and the byte step to head h0 + j (clamped to the last head).
+    const int h0c = min(it.h0, p.num_kv_heads - 1);
+    const uint64_t k_head_b = reinterpret_cast<uint64_t>(p.k) + static_cast<uint64_t>(h0c * p.k_s2 * sizeof(T));
+    const uint64_t v_head_b = reinterpret_cast<uint64_t>(p.v) + static_cast<uint64_t>(h0c * p.v_s2 * sizeof(T));
+    int64_t k_hstep_b[HPW], v_hstep_b[HPW];
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
-        const int64_t hh = min(it.h0 + j, p.num_kv_heads - 1);
-        kh[j] = static_cast<const T*>(p.k) + hh * p.k_s2;
-        vh[j] = static_cast<const T*>(p.v) + hh * p.v_s2;
+        const int64_t dh = min(it.h0 + j, p.num_kv_heads - 1) - h0c;
+        k_hstep_b[j] = dh * p.k_s2 * static_cast<int64_t>(sizeof(T));
+        v_hstep_b[j] = dh * p.v_s2 * static_cast<int64_t>(sizeof(T));
     }
     const bool pow2 = (B & (B - 1)) == 0;
     const int bshift = __builtin_ctz(B);
@@ -339,198 +353,315 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const uint32_t m_lane_b = static_cast<uint32_t>(mask_node * p.words * 8);
     const char* anc_req = reinterpret_cast<const char*>(p.anc + static_cast<int64_t>(qbase) * p.words);
 
-    // Enqueues tile t into `stage`.  Keys past the item's range, and tiles past the
-    // last one, read the tile's first key (finite data, masked later; cache hits), so
-    // every wave issues exactly LPT loads per tile and every load is in bounds.
-    auto issue = [&](int t, int stage) {
+    // A tile's DMA is issued in steps spread over a tile step of the pipeline (so the
+    // eight waves do not all queue on the scalar unit and the load path at once):
+    //   fetch(t)           one iteration ahead: the LDS-cached page number (prefix
+    //                      tile) or this lane's tree slot (tree tile);
+    //   describe(t, f)     the per-lane K and V addresses of tile t (head h0);
+    //   issue_k/v/mask     the loads into a stage (ancestor words for tree tiles only).
+    // Keys past the item's range, and tiles past the last one, read the tile's first
+    // key (finite data, masked later; cache hits), so every load is in bounds and each
+    // wave issues at least 2*HPW loads per tile (the count the waits are based on).
+    auto fetch = [&](int t) -> int {
         const int tt = t < nt ? t : nt - 1;
-        const uint32_t kdst = __builtin_amdgcn_readfirstlane(
-            static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds + stage * TILE_SET + wave * 1024)));
-        const uint32_t mdst = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(
-            reinterpret_cast<uintptr_t>(lds + M_REGION + stage * kMaskBytes + wave * 256)));
         if (tt < ntp) {
-            // Page and first offset of the tile are wave-uniform: scalar arithmetic.
+            const uint32_t tile_pos = static_cast<uint32_t>(it.kbeg + kTileKeys * tt);
+            const uint32_t page_abs = pow2 ? (tile_pos >> bshift) : (tile_pos / static_cast<uint32_t>(B));
+            return pages[page_abs - page0];
+        }
+        const int m0 = kTileKeys * (tt - ntp);
+        int m = m0 + s_key;
+        if (m >= tree_end) m = m0;
+        return tslots[m];
+    };
+    uint64_t dk = 0, dv = 0;   // this lane's K and V chunk addresses of the described tile
+    bool dtree = false;        // described tile is a tree tile
+    uint32_t dmask = 0;        // its ancestor word offset (bytes)
+    auto describe = [&](int t, int fetched) {
+        const int tt = t < nt ? t : nt - 1;
+        if (tt < ntp) {
             const uint32_t tile_pos = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it.kbeg + kTileKeys * tt));
             const uint32_t page_abs = pow2 ? (tile_pos >> bshift) : (tile_pos / static_cast<uint32_t>(B));
-            const int64_t page = __builtin_amdgcn_readfirstlane(pages[page_abs - page0]);
-            const int64_t off0 = tile_pos - page_abs * static_cast<uint32_t>(B);
-            const int64_t kt = page * p.k_s0 + off0 * p.k_s1;
-            const int64_t vt = page * p.v_s0 + off0 * p.v_s1;
+            const uint32_t off0 = tile_pos - page_abs * static_cast<uint32_t>(B);
+            const uint32_t page = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(fetched));
+            const uint64_t kb = k_head_b + static_cast<uint64_t>(page) * k_page_b + static_cast<uint64_t>(off0) * k_key_b;
+            const uint64_t vb = v_head_b + static_cast<uint64_t>(page) * v_page_b + static_cast<uint64_t>(off0) * v_key_b;
             uint32_t kl = k_lane_b, vl = v_lane_b;
             if (static_cast<int>(tile_pos) + kTileKeys > it.kend) {
                 const bool in = static_cast<int>(tile_pos) + s_key < it.kend;
                 kl = in ? kl : k_chunk_b;
                 vl = in ? vl : v_chunk_b;
             }
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) {
-                dma_b128_s(kl, uniform_ptr(kh[j] + kt), kdst + j * kTileBytes);
-                dma_b128_s(vl, uniform_ptr(vh[j] + vt), kdst + V_REGION + j * kTileBytes);
-            }
-            dma_b32_s(m_lane_b, uniform_ptr(anc_req), mdst);
+            dk = kb + kl;
+            dv = vb + vl;
+            dtree = false;
         } else {
-            const int m0 = kTileKeys * (tt - ntp);
-            int m = m0 + s_key;
-            if (m >= tree_end) m = m0;
-            const int slot = tslots[m];
-            const int pg = pow2 ? (slot >> bshift) : (slot / B);
-            const int off = slot - pg * B;
-            const int64_t koff = static_cast<int64_t>(pg) * p.k_s0 + static_cast<int64_t>(off) * p.k_s1 + 8 * k_chunk;
-            const int64_t voff = static_cast<int64_t>(pg) * p.v_s0 + static_cast<int64_t>(off) * p.v_s1 + 8 * v_chunk;
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) {
-                dma_b128(kh[j] + koff, kdst + j * kTileBytes);
-                dma_b128(vh[j] + voff, kdst + V_REGION + j * kTileBytes);
-            }
-            dma_b32_s(m_lane_b, uniform_ptr(anc_req + (m0 >> 5) * 4), mdst);
+            const uint32_t slot = static_cast<uint32_t>(fetched);
+            const uint32_t pg = pow2 ? (slot >> bshift) : (slot / static_cast<uint32_t>(B));
+            const uint32_t off = slot - pg * static_cast<uint32_t>(B);
+            dk = k_head_b + static_cast<uint64_t>(pg) * k_page_b + static_cast<uint64_t>(off) * k_key_b + k_chunk_b;
+            dv = v_head_b + static_cast<uint64_t>(pg) * v_page_b + static_cast<uint64_t>(off) * v_key_b + v_chunk_b;
+            dtree = true;
+            dmask = static_cast<uint32_t>(tt - ntp) * 4;
         }
     };
-
+    auto lds_stage = [&](int offset) {
+        return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds + offset)));
+    };
+    auto issue_k = [&](int stage, int j) {
+        dma_b128(reinterpret_cast<const void*>(dk + k_hstep_b[j]), lds_stage(stage * TILE_SET + wave * 1024 + j * kTileBytes));
+    };
+    auto issue_v = [&](int stage, int j) {
+        dma_b128(reinterpret_cast<const void*>(dv + v_hstep_b[j]),
+                 lds_stage(V_REGION + stage * TILE_SET + wave * 1024 + j * kTileBytes));
+    };
+    auto issue_mask = [&](int stage) {
+        if (dtree) dma_b32_s(m_lane_b, uniform_ptr(anc_req + dmask), lds_stage(M_REGION + stage * kMaskBytes + wave * 256));
+    };
+    auto issue_all = [&](int stage) {
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) issue_k(stage, j);
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) issue_v(stage, j);
+        issue_mask(stage);
+    };
     f32x16 acc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
-    // Per row: reference maximum m_run (score units), its exp2-domain threshold and
-    // offset, and this lane's half of the running sum.
-    float m_run = -INFINITY, thr = -INFINITY, nmc = 0.f, l_run = 0.f;
+    // Per row: reference maximum m_run (score units), -m_run*cs, and this lane's half
+    // of the running sum.
+    float m_run = -INFINITY, nmc = 0.f, l_run = 0.f;
     const float cs = p.c;
     // Tiles [0, nfull) are whole prefix tiles that need no mask.
     const int nfull = (it.kend - it.kbeg) / kTileKeys;
 
-    // Masks tile tt's scores in place, then raises the reference maximum when the
-    // tile exceeds it by 2^8 (rescaling O and the sum, which then hold every earlier
-    // tile).  The decision and the new maximum are taken on the full row (both lane
-    // halves), so the halves of a row always share one reference.
-    auto prepare = [&](f32x16& s, int stage, int tt) {
-        if (tt >= nfull) {
-            // Visibility of the 16 keys this lane holds: key index 8*(v/4) + 4*g + v%4.
-            if (tt < ntp) {
-                const int nvalid = it.kend - (it.kbeg + kTileKeys * tt);
+    // Masks tile tt's scores in place (partial prefix tile and tree tiles only).
+    auto mask_tile = [&](f32x16& s, int stage, int tt) {
+        // Visibility of the 16 keys this lane holds: key index 8*(v/4) + 4*g + v%4.
+        if (tt < ntp) {
+            const int nvalid = it.kend - (it.kbeg + kTileKeys * tt);
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    if (8 * (v >> 2) + 4 * g + (v & 3) >= nvalid) s[v] = -INFINITY;
-                }
-            } else {
-                const uint32_t tree_bits =
-                    row_ok ? *(const __attribute__((address_space(3))) uint32_t*)(lds + m_ofs + stage * kMaskBytes)
-                           : 0u;
-                const uint32_t half_bits = tree_bits >> (4 * g);
+            for (int v = 0; v < 16; ++v) {
+                if (8 * (v >> 2) + 4 * g + (v & 3) >= nvalid) s[v] = -INFINITY;
+            }
+        } else {
+            const uint32_t tree_bits =
+                row_ok ? *(const __attribute__((address_space(3))) uint32_t*)(lds + m_ofs + stage * kMaskBytes) : 0u;
+            const uint32_t half_bits = tree_bits >> (4 * g);
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    if (!((half_bits >> (8 * (v >> 2) + (v & 3))) & 1u)) s[v] = -INFINITY;
-                }
+            for (int v = 0; v < 16; ++v) {
+                if (!((half_bits >> (8 * (v >> 2) + (v & 3))) & 1u)) s[v] = -INFINITY;
             }
         }
+    };
+    // Raises the reference maximum of each row that asks for it (`need` in either lane
+    // half) to the maximum of tile scores `s` where that is larger, rescaling O and
+    // the sum (which then hold every earlier tile).  Both lane halves of a row take the
+    // decision on the full row, so they share one reference; rows that do not ask keep
+    // theirs, so a row's result never depends on other rows' scores.
+    auto raise_max = [&](const f32x16& s, bool need) {
         float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
 #pragma unroll
         for (int v = 3; v < 15; v += 2) mx = fmaxf(fmaxf(mx, s[v]), s[v + 1]);
         mx = fmaxf(mx, s[15]);
-        if (__any(mx * cs > thr)) {
-            const float row_max = fmaxf(mx, __shfl_xor(mx, 32));
-            if (row_max * cs > thr) {
-                const float alpha = __builtin_amdgcn_exp2f((m_run - row_max) * cs);
-                l_run *= alpha;
+        const float row_max = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool row_need = need || __shfl_xor(static_cast<int>(need), 32);
+        if (row_need && row_max > m_run) {
+            const float alpha = __builtin_amdgcn_exp2f((m_run - row_max) * cs);
+            l_run *= alpha;
 #pragma unroll
-                for (int db = 0; db < 4; ++db) acc[db] *= alpha;
-                m_run = row_max;
-                thr = row_max * cs + kRescaleThreshold;
-                nmc = -row_max * cs;
-            }
+            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            m_run = row_max;
+            nmc = -row_max * cs;
         }
     };
+    // Probabilities of tile scores `s` against the current reference, packed as the
+    // P^T operand, and this lane's sum of the packed values.
+    auto probabilities = [&](const f32x16& s, V8 (&pb)[2]) -> float {
+        float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int t8 = 0; t8 < 8; ++t8) {
+                pb[kk][t8] = static_cast<T>(__builtin_amdgcn_exp2f(fmaf(s[8 * kk + t8], cs, nmc)));
+            }
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                const V2 two = {pb[kk][2 * q2], pb[kk][2 * q2 + 1]};
+                if (q2 & 1) l1 = Mfma<T>::dot2(two, l1); else l0 = Mfma<T>::dot2(two, l0);
+            }
+        }
+        return l0 + l1;
+    };
 
-    // One tile step, in a fixed issue order: the 8 QK^T MFMAs of tile t+1 and the 8
-    // P.V MFMAs of tile t alternate with the softmax VALU work of tile t (exp2, bf16
-    // packing, row sums), and every LDS operand is read two MFMA slots ahead of its
-    // use.  Each wave thus keeps its matrix core and its VALU busy at once instead of
-    // running the two phases back to back.
-    auto step = [&](const f32x16& s, f32x16& sn, const int kst, const int vst) {
+    // One tile step of the pipeline, in a fixed issue order: MFMA slots alternate
+    // between the 8 QK^T steps of tile t+1 and the 8 P.V steps of tile t-1 (whose
+    // probabilities were packed in the previous step), every LDS operand is read two
+    // slots ahead of its use, and the softmax VALU work of tile t (exp2, packing, row
+    // sums) fills the slots.  No MFMA of the step waits for a VALU result of the same
+    // step, so the matrix core and the VALU work at once.  piece(slot) adds the DMA
+    // issue of a later tile, a step at a time.
+    auto step = [&](const f32x16& s, f32x16& sn, const V8 (&pb_prev)[2], V8 (&pb)[2], const int kst,
+                    const int vst, auto&& piece) -> float {
         V8 ka[8];
         i16x4 vlo[8], vhi[8];
         float pr[16];
-        V8 pb[2];
         float l0 = 0.f, l1 = 0.f;
         auto kread = [&](int i) {
             ka[i] = __builtin_bit_cast(V8, *(const __attribute__((address_space(3))) u32x4*)(lds + k_ofs[i] + kst));
         };
-        auto vread = [&](int kk, int db) {
-            vlo[4 * kk + db] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        // P.V step j: k half kk = j / 4, output block db = j % 4.
+        auto vread = [&](int j) {
+            const int kk = j >> 2, db = j & 3;
+            vlo[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * kRowBytes));
-            vhi[4 * kk + db] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            vhi[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * kRowBytes));
         };
-        auto qk_mfma = [&](int i) { sn = Mfma<T>::run(ka[i], qb[i], i == 0 ? f32x16{} : sn); };
-        auto pv_mfma = [&](int kk, int db) {
-            const V8 a = __builtin_bit_cast(
-                V8, __builtin_shufflevector(vlo[4 * kk + db], vhi[4 * kk + db], 0, 1, 2, 3, 4, 5, 6, 7));
-            acc[db] = Mfma<T>::run(a, pb[kk], acc[db]);
-        };
-        auto ex = [&](int e) { pr[e] = __builtin_amdgcn_exp2f(fmaf(s[e], cs, nmc)); };
-        auto pack = [&](int kk) {
-#pragma unroll
-            for (int t8 = 0; t8 < 8; ++t8) pb[kk][t8] = static_cast<T>(pr[8 * kk + t8]);
-        };
-        // Row sums from the packed probabilities (the values the P.V product uses).
-        auto rsum = [&](int kk, float& l) {
-#pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                const V2 two = {pb[kk][2 * q2], pb[kk][2 * q2 + 1]};
-                l = Mfma<T>::dot2(two, l);
+        auto slot_mfma = [&](int sl) {
+            if ((sl & 1) == 0) {
+                const int i = sl >> 1;
+                sn = Mfma<T>::run(ka[i], qb[i], i == 0 ? f32x16{} : sn);
+            } else {
+                const int j = sl >> 1, kk = j >> 2, db = j & 3;
+                const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(vlo[j], vhi[j], 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
             }
         };
-        kread(0);
-        kread(1);
+        auto slot_read = [&](int sl) {
+            if ((sl & 1) == 0) kread(sl >> 1); else vread(sl >> 1);
+        };
+        auto ex = [&](int e) {
+            pr[e] = __builtin_amdgcn_exp2f(fmaf(s[e], cs, nmc));
+            pin(pr[e]);
+        };
+        auto pack = [&](int q) {  // probabilities 2q, 2q+1
+            pb[q >> 2][2 * (q & 3)] = static_cast<T>(pr[2 * q]);
+            pb[q >> 2][2 * (q & 3) + 1] = static_cast<T>(pr[2 * q + 1]);
+        };
+        auto rsum = [&](int q) {
+            const V2 two = {pb[q >> 2][2 * (q & 3)], pb[q >> 2][2 * (q & 3) + 1]};
+            if (q & 1) {
+                l1 = Mfma<T>::dot2(two, l1);
+                pin(l1);
+            } else {
+                l0 = Mfma<T>::dot2(two, l0);
+                pin(l0);
+            }
+        };
+        slot_read(0);
+        slot_read(1);
+        ex(0);
+        ex(1);
         order_point();
-        qk_mfma(0); kread(2); ex(0); ex(1); order_point();
-        qk_mfma(1); kread(3); ex(2); ex(3); order_point();
-        qk_mfma(2); kread(4); ex(4); ex(5); order_point();
-        qk_mfma(3); vread(0, 0); ex(6); ex(7); order_point();
-        qk_mfma(4); kread(5); pack(0); ex(8); ex(9); order_point();
-        pv_mfma(0, 0); vread(0, 1); ex(10); ex(11); order_point();
-        qk_mfma(5); kread(6); ex(12); ex(13); order_point();
-        pv_mfma(0, 1); vread(0, 2); ex(14); ex(15); rsum(0, l0); order_point();
-        qk_mfma(6); kread(7); pack(1); order_point();
-        pv_mfma(0, 2); vread(0, 3); rsum(1, l1); order_point();
-        qk_mfma(7); vread(1, 0); order_point();
-        pv_mfma(0, 3); vread(1, 1); order_point();
-        pv_mfma(1, 0); vread(1, 2); order_point();
-        pv_mfma(1, 1); vread(1, 3); order_point();
-        pv_mfma(1, 2); order_point();
-        pv_mfma(1, 3); order_point();
-        l_run += l0 + l1;
+#pragma unroll
+        for (int sl = 0; sl < 16; ++sl) {
+            slot_mfma(sl);
+            if (sl + 2 < 16) slot_read(sl + 2);
+            if (sl < 14) ex(sl + 2);
+            if (sl & 1) pack(sl >> 1);
+            if (!(sl & 1) && sl >= 2) rsum((sl - 2) >> 1);
+            order_point();
+            piece(sl);
+            order_point();
+        }
+        rsum(7);
+        return l0 + l1;
     };
 
-    // Software pipeline over the tiles.  Prologue: tiles 0..NS-2 in flight, scores of
-    // tile 0.  Iteration t: wait for tile t+1 and barrier (publishes every wave's DMA
-    // of tile t+1 and retires stage (t-1)%NS, last read in iteration t-1), enqueue
-    // tile t+NS-1 into that stage, run the tile step (S of tile t+1, softmax and P.V
-    // of tile t), then mask tile t+1 and update the reference maximum.  The loop is
-    // unrolled NS times so every stage offset is a compile-time constant.
+    // Software pipeline over the tiles, three deep: iteration t waits for tile t+1 and
+    // barriers (publishing every wave's DMA of tile t+1 and retiring stage (t-2)%NS,
+    // last read by P.V of tile t-2 in iteration t-1), masks tile t if needed, and runs
+    // the step (S of tile t+1, P.V of tile t-1, softmax of tile t) with the DMA of tile
+    // t+NS-2 into the retired stage.  The reference maximum comes from tile 0 exactly;
+    // later tiles use it as it stands, and only when a tile's probabilities sum past
+    // 2^8 (a score above the reference by more than log2 of that, or a non-finite sum)
+    // is the maximum raised and the tile recomputed, before its P.V is issued.  The
+    // loop is unrolled NS times so every stage offset is a compile-time constant.
+    {
+        // P.V of "tile -1" (iteration 0) multiplies zero probabilities into stage NS-1;
+        // make that stage's V finite.
+        typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 #pragma unroll
-    for (int b = 0; b < NS - 1; ++b) issue(b, b);
-    wait_vmcnt<(NS - 2) * LPT>();
+        for (int i = 0; i < TILE_SET / (16 * kThreads); ++i) {
+            *(lds_u32x4*)(lds + V_REGION + (NS - 1) * TILE_SET + 16 * (tid + i * kThreads)) = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < NS - 2; ++b) {
+        describe(b, fetch(b));
+        issue_all(b);
+    }
+    int pf = fetch(NS - 2);
+    wait_vmcnt<(NS - 3) * LPT>();
     __syncthreads();
     f32x16 s = f32x16{};
+    V8 pb_prev[2];
+    pb_prev[0] = V8{};
+    pb_prev[1] = V8{};
     if (wave_active) {
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             const V8 a = __builtin_bit_cast(V8, *(const __attribute__((address_space(3))) u32x4*)(lds + k_ofs[st]));
             s = Mfma<T>::run(a, qb[st], s);
         }
-        prepare(s, 0, 0);
+        if (nfull == 0) mask_tile(s, 0, 0);
+        raise_max(s, true);
     }
     for (int t0 = 0; t0 < nt; t0 += NS) {
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
             const int t = t0 + b;
             if (t >= nt) break;
-            wait_vmcnt<(NS - 3) * LPT>();
+            wait_vmcnt<(NS - 4) * LPT>();
             __syncthreads();
-            issue(t + NS - 1, (b + NS - 1) % NS);
+            // DMA of tile t+NS-2 into the retired stage, spread over the step's slots.
+            const int ds = (b + NS - 2) % NS;
+            auto piece = [&](int sl) {
+                if (sl == 1) describe(t + NS - 2, pf);
+                if (HPW == 1) {
+                    if (sl == 4) issue_k(ds, 0);
+                    if (sl == 8) issue_v(ds, 0);
+                } else {
+                    if (sl == 3 || sl == 5) issue_k(ds, (sl - 3) >> 1);
+                    if (sl == 7 || sl == 9) issue_v(ds, (sl - 7) >> 1);
+                }
+                if (sl == 12) issue_mask(ds);
+                if (sl == 13) pf = fetch(t + NS - 1);
+            };
             if (wave_active) {
+                if (t >= nfull && t > 0) mask_tile(s, b, t);
                 f32x16 sn;
-                step(s, sn, ((b + 1) % NS) * TILE_SET, b * TILE_SET);
-                if (t + 1 < nt) prepare(sn, (b + 1) % NS, t + 1);
+                V8 pb[2];
+                float lt = step(s, sn, pb_prev, pb, ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET, piece);
+                const bool need = !(lt <= kMaxTileSum);
+                if (__any(need)) {
+                    raise_max(s, need);
+                    lt = probabilities(s, pb);
+                }
+                l_run += lt;
+                pb_prev[0] = pb[0];
+                pb_prev[1] = pb[1];
                 s = sn;
+            } else {
+#pragma unroll
+                for (int sl = 0; sl < 16; ++sl) piece(sl);
+            }
+        }
+    }
+    if (wave_active) {
+        // P.V of the last tile.
+        const uint32_t vst = static_cast<uint32_t>((nt - 1) % NS) * TILE_SET;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * kRowBytes));
+                const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * kRowBytes));
+                const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
             }
         }
     }
@@ -686,6 +817,10 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
     if (a->block_size < 32 || a->block_size % 32) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: block_size %d is not a multiple of 32", a->block_size);
     }
+    // The online softmax orders scores by their value times the scale.
+    if (!(a->scale > 0.f) || !isfinite(a->scale)) {
+        return fail(TV_ERR_UNSUPPORTED, "tree_attention: softmax scale must be positive and finite");
+    }
     if (a->in_dtype != TV_BF16 && a->in_dtype != TV_F16) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: operands must be bf16 or f16");
     }
@@ -701,10 +836,12 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
         !aligned(a->q, 16) || !aligned(a->k_pool, 16) || !aligned(a->v_pool, 16)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: Q/K/V rows must be 16-byte aligned");
     }
-    // Prefix tiles are fetched as page base + per-lane byte offset of up to 31 key rows.
-    if (ks[1] < 0 || vs[1] < 0 || ks[1] * 2 * kTileKeys >= (int64_t{1} << 31) ||
-        vs[1] * 2 * kTileKeys >= (int64_t{1} << 31)) {
-        return fail(TV_ERR_UNSUPPORTED, "tree_attention: K/V slot stride out of range");
+    // Tiles are addressed as page base + per-lane byte offset of up to 31 key rows, with
+    // 32-bit page and key-row byte strides.
+    if (ks[0] < 0 || vs[0] < 0 || ks[1] < 0 || vs[1] < 0 || ks[2] < 0 || vs[2] < 0 ||
+        ks[0] * 2 >= (int64_t{1} << 32) || vs[0] * 2 >= (int64_t{1} << 32) ||
+        ks[1] * 2 * kTileKeys >= (int64_t{1} << 31) || vs[1] * 2 * kTileKeys >= (int64_t{1} << 31)) {
+        return fail(TV_ERR_UNSUPPORTED, "tree_attention: K/V strides out of range");
     }
     if (a->ancestor_words_per_row < 1 || a->ancestor_words_per_row > kMaxTreeSlots / 64) {
         return fail(TV_ERR_INVALID, "tree_attention: ancestor_words_per_row %d out of range",
