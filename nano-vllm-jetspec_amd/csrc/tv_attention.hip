@@ -465,7 +465,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         for (int v = 3; v < 15; v += 2) mx = fmaxf(fmaxf(mx, s[v]), s[v + 1]);
         mx = fmaxf(mx, s[15]);
         const float row_max = fmaxf(mx, __shfl_xor(mx, 32));
-        const bool row_need = need || __shfl_xor(static_cast<int>(need), 32);
+        // Both halves must see the exchange: no short-circuit, which would make the
+        // lane exchange divergent and leave the two halves of a row disagreeing.
+        const int partner_need = __shfl_xor(static_cast<int>(need), 32);
+        const bool row_need = need | (partner_need != 0);
         if (row_need && row_max > m_run) {
             const float alpha = __builtin_amdgcn_exp2f((m_run - row_max) * cs);
             l_run *= alpha;
@@ -716,7 +719,12 @@ tree_attention_kernel(const AttnParams p) {
     }
 }
 
-// Combines the split-K partials of one (request, head group, node block).
+// Combines the split-K partials of one (request, head group, node block).  Grid
+// (groups, 32): workgroup y takes score rows 8y..8y+7 of the group, one thread per
+// (row, 16-byte quad of the head dimension), so the partial loads of all rows are in
+// flight at once.  Each partial holds O unnormalised against its own reference
+// maximum m_s with sum l_s: the result is sum_s w_s O_s / sum_s w_s l_s with
+// w_s = 2^((m_s - max m) * c).
 template <typename T>
 __global__ void __launch_bounds__(256)
 merge_partials_kernel(const AttnParams p) {
@@ -725,29 +733,30 @@ merge_partials_kernel(const AttnParams p) {
     if (r < 0 || r >= p.num_requests) return;
     const int wph = 8 / hpw;
     const int tn = p.cnt[r], qbase = p.cu[r];
-    for (int idx = threadIdx.x; idx < kRowsPerItem * 32; idx += blockDim.x) {
-        const int wr = idx >> 5, quad = idx & 31;
-        const int wave = wr >> 5, c = wr & 31;
-        const int hl = wave / wph;
-        const int head = h0 + hl;
-        const int node = n0 + 8 * (wave - hl * wph) + (c >> 2);
-        if (head >= p.num_kv_heads || node >= tn) continue;
-        const int qh = head * kGroups + (c & 3);
-        float m = -INFINITY;
-        for (int s = 0; s < ns; ++s) m = fmaxf(m, p.ws_ml[static_cast<int64_t>(first + s) * kRowsPerItem + wr].x);
-        const float mc = (m == -INFINITY ? 0.f : m) * p.c;
-        float l = 0.f;
-        f32x4 o = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < ns; ++s) {
-            const int64_t pr = static_cast<int64_t>(first + s) * kRowsPerItem + wr;
-            const float2 ml = p.ws_ml[pr];
-            const float w = __builtin_amdgcn_exp2f(ml.x * p.c - mc);
-            l += ml.y * w;
-            o += *reinterpret_cast<const f32x4*>(p.ws_o + pr * kHeadDim + 4 * quad) * w;
-        }
-        const float inv = 1.f / l;
-        store_out4<T>(p, qbase + node, qh, 4 * quad, o * inv);
+    const int wr = 8 * blockIdx.y + (threadIdx.x >> 5), quad = threadIdx.x & 31;
+    const int wave = wr >> 5, c = wr & 31;
+    const int hl = wave / wph;
+    const int head = h0 + hl;
+    const int node = n0 + 8 * (wave - hl * wph) + (c >> 2);
+    if (head >= p.num_kv_heads || node >= tn) return;
+    const int qh = head * kGroups + (c & 3);
+    const float2* ml = p.ws_ml + static_cast<int64_t>(first) * kRowsPerItem + wr;
+    const float* po = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * kHeadDim + 4 * quad;
+    float m = -INFINITY;
+#pragma unroll 4
+    for (int s = 0; s < ns; ++s) m = fmaxf(m, ml[static_cast<int64_t>(s) * kRowsPerItem].x);
+    const float mc = (m == -INFINITY ? 0.f : m) * p.c;
+    float l = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int s = 0; s < ns; ++s) {
+        const float2 part = ml[static_cast<int64_t>(s) * kRowsPerItem];
+        const float w = __builtin_amdgcn_exp2f(part.x * p.c - mc);
+        l += part.y * w;
+        o += *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s) * kRowsPerItem * kHeadDim) * w;
     }
+    const float inv = 1.f / l;
+    store_out4<T>(p, qbase + node, qh, 4 * quad, o * inv);
 }
 
 __global__ void __launch_bounds__(256)
@@ -907,12 +916,12 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
     if (a->in_dtype == TV_BF16) {
         hipLaunchKernelGGL(tree_attention_kernel<__bf16>, dim3(a->num_items), dim3(kThreads), 0, s, p);
         if (a->num_groups > 0) {
-            hipLaunchKernelGGL(merge_partials_kernel<__bf16>, dim3(a->num_groups), dim3(256), 0, s, p);
+            hipLaunchKernelGGL(merge_partials_kernel<__bf16>, dim3(a->num_groups, kRowsPerItem / 8), dim3(256), 0, s, p);
         }
     } else {
         hipLaunchKernelGGL(tree_attention_kernel<_Float16>, dim3(a->num_items), dim3(kThreads), 0, s, p);
         if (a->num_groups > 0) {
-            hipLaunchKernelGGL(merge_partials_kernel<_Float16>, dim3(a->num_groups), dim3(256), 0, s, p);
+            hipLaunchKernelGGL(merge_partials_kernel<_Float16>, dim3(a->num_groups, kRowsPerItem / 8), dim3(256), 0, s, p);
         }
     }
     return check_launch("tree_attention");

@@ -23,7 +23,7 @@ namespace {
 constexpr int kItemInts = 8;
 constexpr int kRowsPerItem = 256;   // score rows of one workgroup
 constexpr int kHeadDim = 128;
-constexpr int kMinChunkKeys = 256;  // shortest prefix chunk worth a partial result
+constexpr int kMinChunkKeys = 64;   // shortest prefix chunk worth a partial result
 constexpr int kMaxChunkPages = 512; // page numbers a workgroup caches in LDS
 constexpr int kMaxTreeNodes = 1024; // tree slots a workgroup caches in LDS
 

@@ -88,6 +88,22 @@ def test_boundary_prefixes(prefix):
     check_all_rows(q, k, v, meta, f"prefix={prefix}")
 
 
+@pytest.mark.parametrize("counts", [(63, 31, 47), (16, 31, 47)])
+@pytest.mark.parametrize("key", [32, 37, 45, 63])
+def test_score_jump_held_by_one_lane_half(key, counts):
+    """A prefix key in the second tile whose score jumps far above the first tile's for
+    many rows.  Each row's 32 tile keys are split over two lanes; only the lane holding
+    `key` sees the jump, yet the row's reference maximum (and O and the sum) must be
+    raised for both halves together."""
+    q, k, v, meta, *_ = reference_fixture(prefixes=(96, 0, 64), counts=counts)
+    table = meta.block_tables_host[0]
+    slot = table[key // 256] * 256 + key % 256
+    gen = torch.Generator(device=DEV).manual_seed(key)
+    big = 4.0 * torch.randn((k.shape[2], 128), generator=gen, device=DEV)
+    k.view(-1, k.shape[2], 128)[slot] = big.to(k.dtype)
+    check_all_rows(q, k, v, meta, f"jump at key {key}, T={counts[0]}")
+
+
 def test_config2_all_rows_match_oracle():
     batch = workloads.config2(DEV)
     check_all_rows(batch.q, batch.k_pool, batch.v_pool, batch.metadata, "cfg2")
