@@ -57,9 +57,13 @@ def check_m0_discipline(verbose: bool = False) -> None:
         result = subprocess.run(cmd, capture_output=True, text=True)
         if result.returncode != 0:
             raise RuntimeError("hipcc -S failed:\n" + result.stderr)
+        # Explicit M0 operands other than the DMA's own writes, and the instructions that
+        # read M0 implicitly (indexed register moves).
+        implicit = re.compile(r"^\s*(s_set_gpr_idx_on|s_movrel|v_movrel)")
         bad = [line.strip() for line in asm.read_text().splitlines()
-               if re.search(r"\bm0\b", line) and not line.lstrip().startswith(";")
-               and not re.match(r"\s*s_mov_b32 m0, s\d+\s*$", line)]
+               if not line.lstrip().startswith(";")
+               and ((re.search(r"\bm0\b", line) and not re.match(r"\s*s_mov_b32 m0, s\d+\s*$", line))
+                    or implicit.match(line))]
         if bad:
             raise RuntimeError("compiler-generated M0 use would be clobbered by the DMA asm: " + "; ".join(bad[:5]))
         if verbose:
