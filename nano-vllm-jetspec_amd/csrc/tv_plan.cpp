@@ -41,6 +41,49 @@ int heads_per_group(int32_t nodes, int32_t kv_heads) {
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// MI355X dispatches workgroup i of a launch to XCD i % 8, and each XCD has its own L2.
+// The node blocks of one (request, head group, prefix chunk) stream the same K/V, and
+// in longest-first order they sit next to each other, so they would land on different
+// XCDs and each XCD would pull that K/V from HBM.  Within every window of 64 items
+// (8 per XCD), the items of multi-block groups are taken first (keeping their order)
+// and the window is laid out column-major, item i -> position 8 * (i % 8) + i / 8:
+// 8 consecutive items share an XCD and are dispatched together.  Batches without
+// multi-block groups keep the plain longest-first order.
+constexpr int kXcds = 8;
+
+void place_for_xcds(std::vector<Item>& items) {
+    constexpr size_t kWindow = kXcds * kXcds;
+    bool shared = false;
+    for (size_t i = 1; i < items.size() && !shared; ++i) {
+        const Item& a = items[i - 1];
+        const Item& b = items[i];
+        shared = a.r == b.r && a.hg == b.hg && a.chunk == b.chunk;
+    }
+    if (!shared) return;
+    std::vector<Item> window;
+    for (size_t w = 0; w + kWindow <= items.size(); w += kWindow) {
+        window.assign(items.begin() + w, items.begin() + w + kWindow);
+        auto in_group = [&](size_t i) {
+            const Item& x = window[i];
+            auto same = [&](size_t j) {
+                return j < kWindow && window[j].r == x.r && window[j].hg == x.hg && window[j].chunk == x.chunk;
+            };
+            return same(i + 1) || (i > 0 && same(i - 1));
+        };
+        std::vector<Item> order;
+        order.reserve(kWindow);
+        for (size_t i = 0; i < kWindow; ++i) {
+            if (in_group(i)) order.push_back(window[i]);
+        }
+        for (size_t i = 0; i < kWindow; ++i) {
+            if (!in_group(i)) order.push_back(window[i]);
+        }
+        for (size_t i = 0; i < kWindow; ++i) {
+            items[w + kXcds * (i % kXcds) + i / kXcds] = order[i];
+        }
+    }
+}
+
 }  // namespace
 }  // namespace tv
 
@@ -149,6 +192,7 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         if (a.chunk != b.chunk) return a.chunk < b.chunk;
         return a.nb < b.nb;
     });
+    place_for_xcds(items);
     if (items_host) {
         for (size_t i = 0; i < items.size(); ++i) {
             int32_t* o = items_host + kItemInts * i;
