@@ -130,6 +130,52 @@ def copy_probe(torch, gib: int = 2, reps: int = 10) -> dict:
     return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9}
 
 
+def rope_cache(torch, max_positions: int = 40960, dim: int = 128, base: float = 1e6):
+    """Qwen3-8B's cos/sin cache (rope_theta 1e6, 40960 positions) as layers/rotary_embedding.py:28-35 builds it."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2, dtype=torch.float) / dim))
+    freqs = torch.arange(max_positions, dtype=torch.float)[:, None] * inv_freq[None, :]
+    return torch.cat((freqs.cos(), freqs.sin()), dim=-1).unsqueeze_(1).to("cuda")
+
+
+def rope_leg(batch, torch, steps: int, warmup: int) -> dict:
+    """The fused HF-order RoPE + tree K/V scatter (tree_fusion.py:181-199) on the same tree rows.
+
+    Positions are prefix length + node depth; the rotated K and raw V go to the batch's
+    scratch slots, the rotated Q to a separate buffer.  Bytes per row: Q read and written,
+    K and V read and written to the pool, one cos/sin cache row, the position and slot.
+    """
+    from jetspec_amd import rope_scatter_prevalidated, workloads
+
+    meta = batch.metadata
+    positions = torch.tensor([meta.prefix_lengths[r] + d for r in range(meta.num_requests)
+                              for d in workloads.depths_of(batch.parents[r])], dtype=torch.int32, device="cuda")
+    cache = rope_cache(torch)
+    out = torch.empty_like(batch.q)
+    stream = torch.cuda.current_stream()
+
+    def launch():
+        rope_scatter_prevalidated(batch.q, batch.new_k, batch.new_v, positions, cache, batch.k_pool, batch.v_pool,
+                                  meta.tree_slots, out)
+
+    for _ in range(warmup):
+        launch()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    for e in events:
+        e[0].record(stream)
+        launch()
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    rows, hq, dim = batch.q.shape
+    hkv = batch.new_k.shape[1]
+    elem = batch.q.element_size()
+    per_row = 2 * hq * dim * elem + 4 * hkv * dim * elem + dim * cache.element_size() + 4 + meta.tree_slots.element_size()
+    algo = rows * per_row
+    gbs = algo / (ms * 1e-3) / 1e9
+    return {"kernel": "rope_scatter_kernel", "rows": rows, "ms": ms, "algorithmic_bytes": algo, "achieved": gbs,
+            "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS}
+
+
 def run_verify(args, torch):
     from jetspec_amd import packed_tree_attention, read_and_clear_status, store_kvcache, workloads
 
@@ -184,6 +230,7 @@ def run_verify(args, torch):
                      "achieved_tflops": batch.algorithmic_flops() / (attn_ms * 1e-3) / 1e12,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
     }
+    result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
     probe = copy_probe(torch)
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]

@@ -1,7 +1,7 @@
 /*
  * treeverify.h - C ABI of the MI355X (gfx950) tree-verification hot path.
  *
- * Three device operations replace the three Triton/PyTorch operations that the
+ * Four device operations replace the Triton/PyTorch operations that the
  * nano-vllm-jetspec speculative runner calls per verify round:
  *
  *   tv_store_kvcache      slot-mapped K/V append
@@ -14,6 +14,9 @@
  *                         tree_gqa.py:32-111
  *   tv_copy_accepted_kv   accepted-only KV commit across both KV axes and all layers
  *                         replaces speculative/jetspec/state.py:64-86
+ *   tv_rope_scatter       HF-order RoPE of the tree Q/K fused with the scratch
+ *                         scatter of K/V, replaces speculative/jetspec/
+ *                         tree_fusion.py:181-199 (rope_scatter_prevalidated)
  *
  * Conventions
  *   - Every pointer argument is a device pointer unless its name ends in _host.
@@ -50,9 +53,10 @@ enum tv_error {
 enum tv_dtype { TV_BF16 = 0, TV_F16 = 1, TV_F32 = 2 };
 
 enum tv_status_bits {
-    TV_STATUS_BAD_PAGE = 1,    /* a block-table page or tree slot outside the pool */
-    TV_STATUS_BAD_SLOT = 2,    /* a store/commit slot outside the pool */
-    TV_STATUS_BAD_REQUEST = 4  /* metadata row that names a nonexistent request */
+    TV_STATUS_BAD_PAGE = 1,     /* a block-table page or tree slot outside the pool */
+    TV_STATUS_BAD_SLOT = 2,     /* a store/commit slot outside the pool */
+    TV_STATUS_BAD_REQUEST = 4,  /* metadata row that names a nonexistent request */
+    TV_STATUS_BAD_POSITION = 8  /* a RoPE position outside the cos/sin cache */
 };
 
 /* ABI version of the loaded library (TV_ABI_VERSION at build time). */
@@ -108,6 +112,52 @@ int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6],
                         const int64_t* source_slots, const int64_t* destination_slots,
                         int64_t num_slots, void* workspace, int64_t workspace_bytes,
                         int64_t* payload_bytes_host, int32_t* status, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* HF-order RoPE + tree K/V scatter  (speculative/jetspec/tree_fusion.py)     */
+/* ------------------------------------------------------------------------- */
+/*
+ * Replaces rope_scatter_prevalidated (tree_fusion.py:181-199) and its kernel
+ * _rope_scatter_hf_order (tree_fusion.py:20-82); called per layer by
+ * models/qwen3.py:223-240 in place of the eager RoPE + scatter of :241-258.
+ * For every row i < rows, with pos = positions[i] and the cache row
+ * cache[pos] = [cos_0..cos_{D/2-1} | sin_0..sin_{D/2-1}]:
+ *     out[i, h]             = rope(q[i, h])        for every query head h
+ *     k_pool[slot_i, h]     = rope(k[i, h])        for every KV head h
+ *     v_pool[slot_i, h]     = v[i, h]              (bit copy)
+ * where slot_i = node_slots[i] addresses page slot_i / page_size, offset
+ * slot_i % page_size, and rope(x) = [x1*cos - x2*sin | x2*cos + x1*sin] over the
+ * halves x1 = x[:D/2], x2 = x[D/2:] in HF order: for bf16 operands cos/sin are
+ * first rounded to bf16, each of the four products is rounded to bf16 before the
+ * add/subtract, and the result is rounded to bf16 (round to nearest even; a NaN
+ * becomes 0x7FC0); for fp32 operands every product and sum is a separate fp32
+ * operation (no fused multiply-add).
+ * Elements are addressed through element strides (all positive); dtype is
+ * TV_BF16 or TV_F32 for q/k/v/out/pools, cache_dtype TV_BF16 or TV_F32.
+ * Node slots must be unique (one writer per K/V row); a position or slot out of
+ * range sets TV_STATUS_BAD_POSITION / TV_STATUS_BAD_SLOT and that row writes
+ * nothing.
+ */
+typedef struct tv_rope_scatter_args {
+    const void* q;           int64_t q_stride[3];      /* [rows, q_heads, D] */
+    const void* k;           int64_t k_stride[3];      /* [rows, kv_heads, D] */
+    const void* v;           int64_t v_stride[3];
+    const void* positions;   int64_t positions_stride; int32_t positions_is_int64;
+    const void* cache;       int64_t cache_rows, cache_stride_row, cache_stride_elem;
+    int32_t cache_dtype;
+    void* k_pool;            int64_t k_pool_stride[4]; /* [pages, page_size, kv_heads, D] */
+    void* v_pool;            int64_t v_pool_stride[4];
+    int64_t pool_pages, page_size;
+    const void* node_slots;  int64_t slots_stride;     int32_t slots_is_int64;
+    void* out;               int64_t out_stride[3];    /* [rows, q_heads, D] */
+    int64_t rows;
+    int32_t q_heads, kv_heads, head_dim, dtype;
+    int32_t* status;         /* optional */
+} tv_rope_scatter_args;
+
+int64_t tv_sizeof_rope_scatter_args(void);
+
+int tv_rope_scatter(const tv_rope_scatter_args* args, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* packed tree attention  (speculative/jetspec/paged_backend.py:240-306)      */

@@ -6,6 +6,7 @@ Drop-in operators (same names, arguments and errors as the reference):
   copy_accepted_kv        speculative/jetspec/state.py:64-86
   PackedTreeMetadata      speculative/jetspec/packed_metadata.py:16-237
   accept_batch            speculative/jetspec/serving_ops.py:55-90
+  rope_scatter(_prevalidated)  speculative/jetspec/tree_fusion.py:167-199
 Each device operator is a hand-written gfx950 HIP kernel in libtreeverify.so.
 """
 from .packed_metadata import PackedTreeMetadata
@@ -19,6 +20,7 @@ from .paged_backend import (
     paged_tree_attention,
 )
 from .attention import store_kvcache
+from .tree_fusion import rope_scatter, rope_scatter_prevalidated
 from .state import copy_accepted_kv, _slots_for_blocks
 from .serving_ops import accept_batch, accept_walk, build_child_maps
 from ._device import read_and_clear_status
@@ -34,6 +36,8 @@ __all__ = [
     "packed_tree_attention_register_tuned",
     "paged_tree_attention",
     "store_kvcache",
+    "rope_scatter",
+    "rope_scatter_prevalidated",
     "copy_accepted_kv",
     "accept_batch",
     "accept_walk",

@@ -27,6 +27,7 @@ TV_F32 = 2
 TV_STATUS_BAD_PAGE = 1
 TV_STATUS_BAD_SLOT = 2
 TV_STATUS_BAD_REQUEST = 4
+TV_STATUS_BAD_POSITION = 8
 
 # Every extern "C" symbol of include/treeverify.h.
 EXPORTED_SYMBOLS = (
@@ -39,6 +40,8 @@ EXPORTED_SYMBOLS = (
     "tv_tree_attention_plan",
     "tv_pack_ancestor_words",
     "tv_tree_attention",
+    "tv_sizeof_rope_scatter_args",
+    "tv_rope_scatter",
 )
 
 
@@ -93,6 +96,25 @@ class TreeAttentionArgs(ctypes.Structure):
     ]
 
 
+class RopeScatterArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_void_p), ("q_stride", c_int64 * 3),
+        ("k", c_void_p), ("k_stride", c_int64 * 3),
+        ("v", c_void_p), ("v_stride", c_int64 * 3),
+        ("positions", c_void_p), ("positions_stride", c_int64), ("positions_is_int64", c_int32),
+        ("cache", c_void_p), ("cache_rows", c_int64), ("cache_stride_row", c_int64), ("cache_stride_elem", c_int64),
+        ("cache_dtype", c_int32),
+        ("k_pool", c_void_p), ("k_pool_stride", c_int64 * 4),
+        ("v_pool", c_void_p), ("v_pool_stride", c_int64 * 4),
+        ("pool_pages", c_int64), ("page_size", c_int64),
+        ("node_slots", c_void_p), ("slots_stride", c_int64), ("slots_is_int64", c_int32),
+        ("out", c_void_p), ("out_stride", c_int64 * 3),
+        ("rows", c_int64),
+        ("q_heads", c_int32), ("kv_heads", c_int32), ("head_dim", c_int32), ("dtype", c_int32),
+        ("status", c_void_p),
+    ]
+
+
 _lock = threading.Lock()
 _lib = None
 
@@ -122,6 +144,10 @@ def _declare(lib: ctypes.CDLL) -> None:
                                            c_int32, c_void_p, c_void_p, c_void_p]
     lib.tv_tree_attention.restype = c_int32
     lib.tv_tree_attention.argtypes = [POINTER(TreeAttentionArgs), c_void_p]
+    lib.tv_sizeof_rope_scatter_args.restype = c_int64
+    lib.tv_sizeof_rope_scatter_args.argtypes = []
+    lib.tv_rope_scatter.restype = c_int32
+    lib.tv_rope_scatter.argtypes = [POINTER(RopeScatterArgs), c_void_p]
 
 
 def library() -> ctypes.CDLL:
@@ -146,6 +172,8 @@ def library() -> ctypes.CDLL:
             raise RuntimeError(f"libtreeverify ABI {version} != binding ABI {ABI_VERSION}; rebuild it")
         if lib.tv_sizeof_tree_attention_args() != ctypes.sizeof(TreeAttentionArgs):
             raise RuntimeError("tv_tree_attention_args layout differs between library and binding")
+        if lib.tv_sizeof_rope_scatter_args() != ctypes.sizeof(RopeScatterArgs):
+            raise RuntimeError("tv_rope_scatter_args layout differs between library and binding")
         _lib = lib
         return lib
 

@@ -14,10 +14,16 @@ Contents (each restates the cited reference code):
   metadata_arrays       speculative/jetspec/packed_metadata.py:36-126 (host arrays)
   accept_walk           speculative/jetspec/serving_ops.py:55-90
   argmax_flip_witness   benchmarks/jetspec_numeric_oracles.py:171-217
+  rope_scatter_hf       speculative/jetspec/tree_fusion.py:20-82 and the eager HF RoPE
+                        + scatter it replaces, models/qwen3.py:241-258 (numpy, exact
+                        bf16 round-to-nearest-even on uint16 bit patterns)
 
 Pinning: tests/test_oracle_pins.py checks every function above against the
 reference's own known-answer tests (transcribed into tests/golden/reference_kats.json),
 closed forms and an independent brute force; see the header of that file.
+rope_scatter_hf is pinned against torch's eager CPU bf16/fp32 arithmetic, which is the
+expected value of the reference's own test (tests/test_jetspec_tree_fusion.py:21-32),
+and against the reference's rounding witness (:117-126).
 """
 from __future__ import annotations
 
@@ -292,3 +298,68 @@ def argmax_flip_witness(actual: np.ndarray, reference: np.ndarray) -> dict:
         flips += int(flipped)
         violations += int(flipped and not consistent)
     return {"rows_checked": a.shape[0], "argmax_flips": flips, "large_margin_violations": violations}
+
+
+# --------------------------------------------------------------------------- HF-order RoPE + scatter
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    """uint16 bf16 bit patterns -> float32 values (exact)."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def f32_to_bf16_bits(values: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits, round to nearest even; any NaN -> 0x7FC0 (c10 BFloat16 rounding)."""
+    x = np.asarray(values, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    rounded = ((u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)).astype(np.uint16)
+    return np.where(np.isnan(x), np.uint16(0x7FC0), rounded)
+
+
+def _round_bf16(values: np.ndarray) -> np.ndarray:
+    return bf16_bits_to_f32(f32_to_bf16_bits(values))
+
+
+def rope_hf_order(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, bf16: bool) -> np.ndarray:
+    """Eager HF RoPE of float32 values `x` [..., D] with cos/sin [..., D/2] (qwen3.py:241-249).
+
+    bf16: cos/sin are rounded to bf16, every product is rounded to bf16 before the
+    add/subtract and the result is rounded to bf16 (tree_fusion.py:21-28); returns bf16
+    values as float32.  fp32: separate fp32 products and sums (no fused multiply-add).
+    """
+    half = x.shape[-1] // 2
+    x1, x2 = x[..., :half].astype(np.float32), x[..., half:].astype(np.float32)
+    cos = np.asarray(cos, dtype=np.float32)
+    sin = np.asarray(sin, dtype=np.float32)
+    if bf16:
+        with np.errstate(all="ignore"):
+            cos, sin = _round_bf16(cos), _round_bf16(sin)
+            a, b = _round_bf16(x1 * cos), _round_bf16(x2 * sin)
+            c, d = _round_bf16(x2 * cos), _round_bf16(x1 * sin)
+            return np.concatenate((_round_bf16(a - b), _round_bf16(c + d)), axis=-1)
+    with np.errstate(all="ignore"):
+        y1 = (x1 * cos).astype(np.float32) - (x2 * sin).astype(np.float32)
+        y2 = (x2 * cos).astype(np.float32) + (x1 * sin).astype(np.float32)
+    return np.concatenate((y1, y2), axis=-1).astype(np.float32)
+
+
+def rope_scatter_hf(q, k, v, positions, cache, k_pool, v_pool, node_slots, bf16: bool):
+    """Rotated Q, and K/V pools with the rotated K / raw V rows scattered (tree_fusion.py:42-82).
+
+    q/k/v: float32 values [rows, heads, D] (bf16 operands given as their exact float32
+    values); cache: float32 [positions, D] rows [cos | sin] (a bf16 cache as its float32
+    values); k_pool/v_pool: [pages, page_size, kv_heads, D] arrays, updated in place;
+    node_slots: unique slots.  Returns the rotated Q as float32 values.
+    """
+    positions = np.asarray(positions, dtype=np.int64)
+    slots = np.asarray(node_slots, dtype=np.int64)
+    rows = cache[positions]
+    half = q.shape[-1] // 2
+    cos, sin = rows[:, None, :half], rows[:, None, half:]
+    with np.errstate(all="ignore"):
+        out_q = rope_hf_order(q, cos, sin, bf16)
+        out_k = rope_hf_order(k, cos, sin, bf16)
+    page_size = k_pool.shape[1]
+    pages, offsets = slots // page_size, slots % page_size
+    k_pool[pages, offsets] = out_k
+    v_pool[pages, offsets] = v
+    return out_q
+
