@@ -176,6 +176,44 @@ def rope_leg(batch, torch, steps: int, warmup: int) -> dict:
             "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS}
 
 
+def accept_leg(batch, torch, steps: int, warmup: int, vocab: int = 151936) -> dict:
+    """Greedy acceptance on the device for the same tree rows: the argmax over Qwen3's
+    vocabulary (bf16 synthetic logits) and the per-request walk.  torch.argmax on the same
+    logits is timed beside it (the reference's own device step, serving_ops.py:62)."""
+    from jetspec_amd import accept_batch_device, greedy_argmax, workloads
+
+    meta = batch.metadata
+    rows = meta.total_queries
+    logits = torch.randn(rows, vocab, device="cuda", dtype=torch.bfloat16)
+    tokens = torch.randint(0, vocab, (rows,), device="cuda")
+    parents = torch.tensor([p for r in range(meta.num_requests) for p in batch.parents[r]], device="cuda")
+    depths = torch.tensor([d for r in range(meta.num_requests) for d in workloads.depths_of(batch.parents[r])],
+                          device="cuda")
+    cu = meta.cu_seqlens_q
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+        for e in events:
+            e[0].record(stream)
+            fn()
+            e[1].record(stream)
+        torch.cuda.synchronize()
+        return statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+
+    argmax_ms = timed(lambda: greedy_argmax(logits))
+    torch_ms = timed(lambda: logits.argmax(-1))
+    accept_ms = timed(lambda: accept_batch_device(logits, tokens, parents, depths, cu, 15))
+    algo = rows * vocab * logits.element_size()
+    gbs = algo / (argmax_ms * 1e-3) / 1e9
+    del logits
+    return {"kernel": "argmax_rows_kernel", "rows": rows, "vocab": vocab, "argmax_ms": argmax_ms,
+            "torch_argmax_ms": torch_ms, "argmax_plus_walk_ms": accept_ms, "algorithmic_bytes": algo,
+            "achieved": gbs, "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS}
+
+
 def run_verify(args, torch):
     from jetspec_amd import packed_tree_attention, read_and_clear_status, store_kvcache, workloads
 
@@ -231,6 +269,7 @@ def run_verify(args, torch):
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
     }
     result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
+    result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
     probe = copy_probe(torch)
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]

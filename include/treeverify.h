@@ -1,7 +1,7 @@
 /*
  * treeverify.h - C ABI of the MI355X (gfx950) tree-verification hot path.
  *
- * Four device operations replace the Triton/PyTorch operations that the
+ * These device operations replace the Triton/PyTorch operations that the
  * nano-vllm-jetspec speculative runner calls per verify round:
  *
  *   tv_store_kvcache      slot-mapped K/V append
@@ -17,6 +17,8 @@
  *   tv_rope_scatter       HF-order RoPE of the tree Q/K fused with the scratch
  *                         scatter of K/V, replaces speculative/jetspec/
  *                         tree_fusion.py:181-199 (rope_scatter_prevalidated)
+ *   tv_argmax_rows,       greedy acceptance: the target argmax and the tree walk,
+ *   tv_tree_accept        replaces speculative/jetspec/serving_ops.py:55-90
  *
  * Conventions
  *   - Every pointer argument is a device pointer unless its name ends in _host.
@@ -56,7 +58,8 @@ enum tv_status_bits {
     TV_STATUS_BAD_PAGE = 1,     /* a block-table page or tree slot outside the pool */
     TV_STATUS_BAD_SLOT = 2,     /* a store/commit slot outside the pool */
     TV_STATUS_BAD_REQUEST = 4,  /* metadata row that names a nonexistent request */
-    TV_STATUS_BAD_POSITION = 8  /* a RoPE position outside the cos/sin cache */
+    TV_STATUS_BAD_POSITION = 8, /* a RoPE position outside the cos/sin cache */
+    TV_STATUS_BAD_DEPTH = 16    /* an accepted path node off its canonical depth */
 };
 
 /* ABI version of the loaded library (TV_ABI_VERSION at build time). */
@@ -158,6 +161,36 @@ typedef struct tv_rope_scatter_args {
 int64_t tv_sizeof_rope_scatter_args(void);
 
 int tv_rope_scatter(const tv_rope_scatter_args* args, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* greedy acceptance  (speculative/jetspec/serving_ops.py:55-90)              */
+/* ------------------------------------------------------------------------- */
+/*
+ * out[r] = argmax_j logits[r * row_stride + j], j < vocab, in torch.argmax's order
+ * (a NaN beats every number; equal values, or two NaNs, go to the lower index).
+ * Replaces the `logits.argmax(-1)` of serving_ops.py:62.  dtype TV_BF16 or TV_F32.
+ */
+int tv_argmax_rows(const void* logits, int64_t rows, int64_t vocab, int64_t row_stride,
+                   int32_t dtype, int64_t* out, void* stream);
+
+/*
+ * The per-request greedy walk of serving_ops.py:78-89 on the device.  Request r owns
+ * packed rows [cu_seqlens[r], cu_seqlens[r+1]) holding its tree nodes in order
+ * (node 0 = root); token_ids/parents/depths are per node (parents request-local,
+ * -1 at the root), greedy is the per-row argmax.  From the root, the next node is
+ * the child of the current node whose token equals greedy[current]; among sibling
+ * nodes with that token the last one wins.  The walk stops at a miss or after
+ * max_depth + 1 path nodes.  Writes paths[r * (max_depth + 1) + i] (root-inclusive,
+ * -1 padded), lengths[r] = path nodes - 1 and corrections[r] = greedy of the last
+ * path node.  A path node whose depth differs from its path index sets
+ * TV_STATUS_BAD_DEPTH (the reference raises RuntimeError, serving_ops.py:84-85).
+ */
+int tv_tree_accept(const int64_t* greedy, const void* token_ids, int32_t tokens_is_int64,
+                   const void* parents, int32_t parents_is_int64,
+                   const void* depths, int32_t depths_is_int64,
+                   const int32_t* cu_seqlens, int32_t num_requests, int32_t max_depth,
+                   int32_t* paths, int32_t* lengths, int64_t* corrections,
+                   int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* packed tree attention  (speculative/jetspec/paged_backend.py:240-306)      */

@@ -1,0 +1,249 @@
+// Greedy tree acceptance on the device, for gfx950: the per-row argmax of the target
+// logits and the per-request walk down the draft tree (serving_ops.py:55-90).
+//
+// argmax_rows_kernel: one 256-thread workgroup per logits row, 16-byte loads, each
+// thread scanning its elements in increasing index order, then a wave and a workgroup
+// reduction.  The order is torch.argmax's (ATen's GreaterOrNan): a NaN beats every
+// number, and between equal values (or two NaNs) the lower index wins.  The kernel is
+// HBM-bound: rows x vocab x element bytes, read once.
+//
+// tree_accept_kernel: one wave per request.  From the root, the next node is the child
+// of the current node whose token equals the current node's argmax; among duplicate
+// sibling tokens the last child wins (the child_maps rule, serving_ops.py:58-59).  The
+// walk stops at a miss or after max_depth + 1 nodes, and every node on the path must
+// sit at the depth equal to its path index (serving_ops.py:84-85), else the request is
+// flagged.  The 64 lanes scan the request's nodes for the matching child in parallel.
+#include <math.h>
+#include <stdint.h>
+
+#include "tv_internal.h"
+
+namespace tv {
+namespace {
+
+constexpr int kArgmaxThreads = 256;
+
+// a beats b under torch's ordering (GreaterOrNan).
+__device__ __forceinline__ bool beats(float a, int64_t ia, float b, int64_t ib) {
+    const bool na = a != a, nb = b != b;
+    if (na) return nb ? ia < ib : true;
+    if (nb) return false;
+    return a == b ? ia < ib : a > b;
+}
+
+__device__ __forceinline__ float elem_value(const uint16_t* p, int64_t i) {
+    return __uint_as_float(static_cast<uint32_t>(p[i]) << 16);
+}
+__device__ __forceinline__ float elem_value(const float* p, int64_t i) { return p[i]; }
+
+// Unit: 8 bf16 or 4 fp32 per 16-byte load (Vec > 1), or one element.  Each thread
+// visits its elements in increasing index order, so within a thread a later element
+// replaces the best one only if it is larger, or a NaN replacing a number: equal
+// values and later NaNs keep the earlier index.  Four loads are issued per iteration
+// so that each wave keeps several in flight.
+template <typename S, int VEC>
+__global__ void __launch_bounds__(kArgmaxThreads)
+argmax_rows_kernel(const S* __restrict__ logits, int64_t row_stride, int64_t vocab, int64_t* __restrict__ out) {
+    constexpr int kUnroll = 4;
+    const int64_t row = blockIdx.x;
+    const S* base = logits + row * row_stride;
+    float best = -INFINITY;
+    int64_t best_i = INT64_MAX;
+    bool any = false;
+    auto visit = [&](float v, int64_t i) {
+        const bool take = !any || v > best || (v != v && best == best);
+        best = take ? v : best;
+        best_i = take ? i : best_i;
+        any = true;
+    };
+    // Full vector units first (VEC elements each), then the scalar tail.
+    const int64_t units = VEC > 1 ? vocab / VEC : 0;
+    for (int64_t u0 = threadIdx.x; u0 < units; u0 += kUnroll * kArgmaxThreads) {
+        u32x4 raw[kUnroll];
+#pragma unroll
+        for (int k = 0; k < kUnroll; ++k) {
+            const int64_t u = u0 + k * kArgmaxThreads;
+            if (u < units) raw[k] = *reinterpret_cast<const u32x4*>(base + u * VEC);
+        }
+#pragma unroll
+        for (int k = 0; k < kUnroll; ++k) {
+            const int64_t u = u0 + k * kArgmaxThreads;
+            if (u < units) {
+                S vals[VEC];
+                __builtin_memcpy(vals, &raw[k], 16);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) visit(elem_value(vals, e), u * VEC + e);
+            }
+        }
+    }
+    for (int64_t i = units * VEC + threadIdx.x; i < vocab; i += kArgmaxThreads) visit(elem_value(base, i), i);
+    // Wave reduction (64 lanes), then across the 4 waves through LDS.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int64_t oi = __shfl_xor(best_i, off);
+        const bool oany = __shfl_xor(static_cast<int>(any), off) != 0;
+        if (oany && (!any || beats(ov, oi, best, best_i))) {
+            best = ov;
+            best_i = oi;
+            any = true;
+        }
+    }
+    __shared__ float wave_best[kArgmaxThreads / 64];
+    __shared__ int64_t wave_idx[kArgmaxThreads / 64];
+    __shared__ int wave_any[kArgmaxThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        wave_best[wave] = best;
+        wave_idx[wave] = best_i;
+        wave_any[wave] = any;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = wave_best[0];
+        int64_t bi = wave_idx[0];
+        bool ba = wave_any[0] != 0;
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) {
+            if (wave_any[w] && (!ba || beats(wave_best[w], wave_idx[w], b, bi))) {
+                b = wave_best[w];
+                bi = wave_idx[w];
+                ba = true;
+            }
+        }
+        out[row] = ba ? bi : 0;
+    }
+}
+
+template <typename I>
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i) {
+    return static_cast<int64_t>(static_cast<const I*>(p)[i]);
+}
+
+__device__ __forceinline__ int64_t load_int(const void* p, int is64, int64_t i) {
+    return is64 ? load_index<int64_t>(p, i) : load_index<int32_t>(p, i);
+}
+
+struct AcceptParams {
+    const int64_t* greedy;     // [Q] argmax per packed row
+    const void* tokens;        // [Q] draft token of each node
+    const void* parents;       // [Q] request-local parent (-1 at the root)
+    const void* depths;        // [Q] depth of each node
+    int32_t tokens64, parents64, depths64;
+    const int32_t* cu;         // [R + 1] packed row offsets
+    int32_t num_requests, max_depth;
+    int32_t* paths;            // [R, max_depth + 1] root-inclusive path, -1 padded
+    int32_t* lengths;          // [R] accepted draft length = path nodes - 1
+    int64_t* corrections;      // [R] greedy token at the last path node
+    int32_t* status;
+};
+
+__global__ void __launch_bounds__(64)
+tree_accept_kernel(const AcceptParams p) {
+    const int r = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int lo = p.cu[r], hi = p.cu[r + 1];
+    const int n = hi - lo;
+    const int width = p.max_depth + 1;
+    int32_t* path = p.paths + static_cast<int64_t>(r) * width;
+    for (int i = lane; i < width; i += 64) path[i] = -1;
+    if (n < 1) {
+        if (lane == 0) {
+            set_status(p.status, TV_STATUS_BAD_REQUEST);
+            p.lengths[r] = -1;
+            p.corrections[r] = -1;
+        }
+        return;
+    }
+    int node = 0, count = 1;
+    bool depth_ok = load_int(p.depths, p.depths64, lo) == 0;
+    if (lane == 0) path[0] = 0;
+    while (count <= p.max_depth) {
+        const int64_t want = p.greedy[lo + node];
+        int found = -1;
+        for (int m = 1 + lane; m < n; m += 64) {
+            if (load_int(p.parents, p.parents64, lo + m) == node && load_int(p.tokens, p.tokens64, lo + m) == want) {
+                found = m;   // increasing m per lane: the lane keeps its last match
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) found = max(found, __shfl_xor(found, off));
+        if (found < 0) break;
+        node = found;
+        if (lane == 0) path[count] = node;
+        depth_ok = depth_ok && load_int(p.depths, p.depths64, lo + node) == count;
+        ++count;
+    }
+    if (lane == 0) {
+        p.lengths[r] = count - 1;
+        p.corrections[r] = p.greedy[lo + node];
+        if (!depth_ok) set_status(p.status, TV_STATUS_BAD_DEPTH);
+    }
+}
+
+}  // namespace
+}  // namespace tv
+
+using namespace tv;
+
+extern "C" int tv_argmax_rows(const void* logits, int64_t rows, int64_t vocab, int64_t row_stride, int32_t dtype,
+                              int64_t* out, void* stream) {
+    clear_error();
+    if (rows < 0 || vocab < 1 || row_stride < vocab) return fail(TV_ERR_INVALID, "argmax_rows: invalid sizes");
+    if (dtype != TV_BF16 && dtype != TV_F32) return fail(TV_ERR_UNSUPPORTED, "argmax_rows: logits must be bf16 or fp32");
+    if (rows == 0) return TV_OK;
+    if (rows > 0x7fffffff) return fail(TV_ERR_UNSUPPORTED, "argmax_rows: too many rows");
+    if (!logits || !out) return fail(TV_ERR_INVALID, "argmax_rows: null pointer");
+    const int64_t elem = dtype == TV_F32 ? 4 : 2;
+    const bool vec = aligned(logits, 16) && (row_stride * elem) % 16 == 0;
+    hipStream_t s = as_stream(stream);
+    if (dtype == TV_BF16) {
+        if (vec) {
+            hipLaunchKernelGGL((argmax_rows_kernel<uint16_t, 8>), dim3(rows), dim3(kArgmaxThreads), 0, s,
+                               static_cast<const uint16_t*>(logits), row_stride, vocab, out);
+        } else {
+            hipLaunchKernelGGL((argmax_rows_kernel<uint16_t, 1>), dim3(rows), dim3(kArgmaxThreads), 0, s,
+                               static_cast<const uint16_t*>(logits), row_stride, vocab, out);
+        }
+    } else {
+        if (vec) {
+            hipLaunchKernelGGL((argmax_rows_kernel<float, 4>), dim3(rows), dim3(kArgmaxThreads), 0, s,
+                               static_cast<const float*>(logits), row_stride, vocab, out);
+        } else {
+            hipLaunchKernelGGL((argmax_rows_kernel<float, 1>), dim3(rows), dim3(kArgmaxThreads), 0, s,
+                               static_cast<const float*>(logits), row_stride, vocab, out);
+        }
+    }
+    return check_launch("argmax_rows");
+}
+
+extern "C" int tv_tree_accept(const int64_t* greedy, const void* token_ids, int32_t tokens_is_int64,
+                              const void* parents, int32_t parents_is_int64, const void* depths,
+                              int32_t depths_is_int64, const int32_t* cu_seqlens, int32_t num_requests,
+                              int32_t max_depth, int32_t* paths, int32_t* lengths, int64_t* corrections,
+                              int32_t* status, void* stream) {
+    clear_error();
+    if (num_requests < 0 || max_depth < 0 || max_depth > 4096) {
+        return fail(TV_ERR_INVALID, "tree_accept: invalid request count or max_depth");
+    }
+    if (num_requests == 0) return TV_OK;
+    if (!greedy || !token_ids || !parents || !depths || !cu_seqlens || !paths || !lengths || !corrections) {
+        return fail(TV_ERR_INVALID, "tree_accept: null pointer");
+    }
+    AcceptParams p;
+    p.greedy = greedy;
+    p.tokens = token_ids;
+    p.parents = parents;
+    p.depths = depths;
+    p.tokens64 = tokens_is_int64 != 0;
+    p.parents64 = parents_is_int64 != 0;
+    p.depths64 = depths_is_int64 != 0;
+    p.cu = cu_seqlens;
+    p.num_requests = num_requests;
+    p.max_depth = max_depth;
+    p.paths = paths;
+    p.lengths = lengths;
+    p.corrections = corrections;
+    p.status = status;
+    hipLaunchKernelGGL(tree_accept_kernel, dim3(num_requests), dim3(64), 0, as_stream(stream), p);
+    return check_launch("tree_accept");
+}

@@ -28,6 +28,7 @@ TV_STATUS_BAD_PAGE = 1
 TV_STATUS_BAD_SLOT = 2
 TV_STATUS_BAD_REQUEST = 4
 TV_STATUS_BAD_POSITION = 8
+TV_STATUS_BAD_DEPTH = 16
 
 # Every extern "C" symbol of include/treeverify.h.
 EXPORTED_SYMBOLS = (
@@ -42,6 +43,8 @@ EXPORTED_SYMBOLS = (
     "tv_tree_attention",
     "tv_sizeof_rope_scatter_args",
     "tv_rope_scatter",
+    "tv_argmax_rows",
+    "tv_tree_accept",
 )
 
 
@@ -148,6 +151,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_sizeof_rope_scatter_args.argtypes = []
     lib.tv_rope_scatter.restype = c_int32
     lib.tv_rope_scatter.argtypes = [POINTER(RopeScatterArgs), c_void_p]
+    lib.tv_argmax_rows.restype = c_int32
+    lib.tv_argmax_rows.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_void_p, c_void_p]
+    lib.tv_tree_accept.restype = c_int32
+    lib.tv_tree_accept.argtypes = [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_int32, c_void_p,
+                                   c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
 
 
 def library() -> ctypes.CDLL:

@@ -1,0 +1,151 @@
+"""Device greedy acceptance (tv_argmax_rows + tv_tree_accept) on the GPU.
+
+The argmax must equal torch.argmax index for index (ties to the lower index, NaN
+first), at the served shape (4096 tree rows x Qwen3's 151936-token vocabulary, bf16)
+and on edge rows.  The walks must equal the oracle's host walk (restating
+serving_ops.py:78-89) on random trees with duplicate sibling tokens, the reference's
+duplicate-sibling KAT (tests/test_jetspec_serving_ops.py:39-58), depth truncation,
+and must raise on a path that leaves the canonical depths.
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from jetspec_amd import accept_batch, accept_batch_device, greedy_argmax, workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("rows,vocab", [(1, 1), (3, 7), (17, 1000), (64, 4099), (4096, 151936)])
+def test_argmax_equals_torch(dtype, rows, vocab):
+    print(f"[argmax] dtype={dtype} rows={rows} vocab={vocab}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(rows * 7 + vocab)
+    logits = torch.randn(rows, vocab, generator=g, device=DEV).to(dtype)
+    got = greedy_argmax(logits)
+    assert torch.equal(got, logits.argmax(-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_argmax_edge_rows(dtype):
+    vocab = 3001
+    logits = torch.randn(12, vocab, device=DEV).to(dtype)
+    logits[0] = 1.5                                        # all equal -> 0
+    logits[1] = float("-inf")                              # all -inf -> 0
+    logits[2, 17] = logits[2, 2000] = 1e4                  # tie -> lower index
+    logits[3, 5] = float("nan")                            # NaN wins
+    logits[4, 9] = logits[4, 3000] = float("nan")          # first NaN
+    logits[4, 100] = float("inf")
+    logits[5, 3000] = float("inf")                         # last element, the scalar tail
+    logits[6] = 0.0
+    logits[6, 2999] = -0.0
+    logits[7, 1:] = -1.0
+    logits[7, 0] = -0.5                                    # first element
+    logits[8, 2048] = 7e3                                  # vector-unit boundary
+    logits[9, 2047] = logits[9, 2049] = 7e3
+    logits[10] = float("-inf")
+    logits[10, 1234] = -3e38 if dtype == torch.float32 else -3.0e38
+    logits[11, ::2] = 2.0                                  # many ties
+    got = greedy_argmax(logits)
+    assert torch.equal(got, logits.argmax(-1))
+
+
+def test_argmax_strided_rows():
+    backing = torch.randn(40, 5003, device=DEV, dtype=torch.bfloat16)
+    view = backing[::3, 1:4998]                            # unaligned start, row stride 3 * 5003
+    assert torch.equal(greedy_argmax(view), view.argmax(-1))
+
+
+def random_batch(rng, sizes, vocab=6, max_depth=8):
+    trees, offsets = [], [0]
+    for n in sizes:
+        parents = workloads.random_parents(n, max_depth, rng)
+        tokens = [int(t) for t in rng.integers(0, vocab, size=n)]
+        depths = workloads.depths_of(parents)
+        trees.append(SimpleNamespace(num_nodes=n, host_token_ids=tokens, host_parents=parents, host_depths=depths,
+                                     child_maps=oracle.child_maps(tokens, parents),
+                                     token_ids=torch.tensor(tokens, device=DEV),
+                                     parent_indices=torch.tensor(parents, device=DEV),
+                                     depth=torch.tensor(depths, device=DEV)))
+        offsets.append(offsets[-1] + n)
+    return trees, offsets
+
+
+@pytest.mark.parametrize("max_depth", [0, 3, 15])
+def test_walks_equal_oracle_walks(max_depth):
+    rng = np.random.default_rng(11 + max_depth)
+    sizes = [1, 2, 16, 31, 32, 64, 65, 200, 1024]
+    trees, offsets = random_batch(rng, sizes)
+    vocab = 6
+    logits = torch.randn(offsets[-1], vocab, device=DEV)
+    # Bias each node's argmax towards one of its children's tokens so walks go deep.
+    for tree, lo in zip(trees, offsets):
+        for node, children in enumerate(tree.child_maps):
+            if children and rng.random() < 0.85:
+                logits[lo + node, int(rng.choice(list(children)))] += 6.0
+    results = accept_batch(logits, trees, offsets, max_depth)
+    greedy = logits.argmax(-1).tolist()
+    deepest = 0
+    for i, tree in enumerate(trees):
+        want = oracle.accept_walk(greedy[offsets[i]:offsets[i + 1]], tree.host_token_ids, tree.host_depths,
+                                  tree.child_maps, max_depth)
+        assert results[i] == want, f"request {i} ({sizes[i]} nodes)"
+        deepest = max(deepest, want["accepted_length"])
+    assert deepest >= min(max_depth, 3), "the biased logits should drive some walk deep"
+
+
+def test_duplicate_sibling_kat_last_child_wins():
+    kat = KATS["accept_duplicate_siblings"]
+    tree = SimpleNamespace(token_ids=torch.tensor(kat["tokens"], device=DEV),
+                           parent_indices=torch.tensor(kat["parents"], device=DEV),
+                           depth=torch.tensor(kat["depths"], device=DEV), num_nodes=len(kat["tokens"]))
+    logits = torch.randn(len(kat["tokens"]), 80, generator=torch.Generator().manual_seed(99)).to(DEV)
+    for node, token in kat["forced_argmax"].items():
+        logits[int(node), token] = 100
+    result = accept_batch(logits, [tree], [0, len(kat["tokens"])], kat["max_depth"])[0]
+    assert result["path"] == kat["expected_path"]
+    assert result["accepted_length"] == len(kat["expected_path"]) - 1
+    assert result["correction"] == int(logits[kat["expected_path"][-1]].argmax())
+
+
+def test_device_outputs_without_host_walk():
+    rng = np.random.default_rng(3)
+    trees, offsets = random_batch(rng, [16, 64, 5])
+    logits = torch.randn(offsets[-1], 6, device=DEV, dtype=torch.bfloat16)
+    tokens = torch.cat([t.token_ids for t in trees])
+    parents = torch.cat([t.parent_indices for t in trees]).to(torch.int32)
+    depths = torch.cat([t.depth for t in trees])
+    cu = torch.tensor(offsets, dtype=torch.int32, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    greedy, paths, lengths, corrections = accept_batch_device(logits, tokens, parents, depths, cu, 15, status=status)
+    assert torch.equal(greedy, logits.argmax(-1))
+    host = greedy.tolist()
+    for i, tree in enumerate(trees):
+        want = oracle.accept_walk(host[offsets[i]:offsets[i + 1]], tree.host_token_ids, tree.host_depths,
+                                  tree.child_maps, 15)
+        n = want["accepted_length"] + 1
+        assert paths[i, :n].tolist() == want["path"] and (paths[i, n:] == -1).all()
+        assert int(lengths[i]) == want["accepted_length"] and int(corrections[i]) == want["correction"]
+    assert int(status) == 0
+
+
+def test_noncanonical_depth_raises():
+    rng = np.random.default_rng(8)
+    trees, offsets = random_batch(rng, [16])
+    tree = trees[0]
+    child = next(iter(tree.child_maps[0].values()))
+    tree.host_depths = list(tree.host_depths)
+    tree.host_depths[child] = 5                     # off its canonical depth 1
+    logits = torch.full((16, 6), -1.0, device=DEV)
+    logits[0, tree.host_token_ids[child]] = 1.0     # the walk takes that child
+    with pytest.raises(RuntimeError, match="canonical tail"):
+        accept_batch(logits, trees, offsets, 15)
