@@ -234,6 +234,30 @@ int tv_pack_ancestor_words(const float* qq_bias, const int64_t* qq_bias_offsets,
                            int32_t num_requests, int32_t words_per_row,
                            uint64_t* words, int32_t* status, void* stream);
 
+/*
+ * Device-side construction of the same bits from the tree topology, replacing the
+ * host-built f32 bias of packed_metadata.py:185-195 on the serving path: parents
+ * holds every packed node's request-local parent (-1 at node 0, else < the node),
+ * request r owns rows [cu_seqlens[r], cu_seqlens[r+1]) with at most max_nodes
+ * (<= 1024) nodes, and words_per_row >= ceil(max_nodes / 64) (<= 16).
+ * words[q * words_per_row + w] bit b is set iff node 64w + b is q itself or one of
+ * its ancestors.  A malformed parent sets TV_STATUS_BAD_REQUEST (that node is then
+ * treated as a root).
+ */
+int tv_ancestor_words_from_parents(const int32_t* parents, const int32_t* cu_seqlens,
+                                   int32_t num_requests, int32_t max_nodes, int32_t words_per_row,
+                                   uint64_t* words, int32_t* status, void* stream);
+
+/*
+ * The reference's additive bias (packed_metadata.py:96-100) from ancestor words:
+ * qq_bias[qq_bias_offsets[r] + i * T + m] = 0 if bit m of row (r, i) is set, else
+ * -inf, for every packed row q = (query_to_request[q], query_local_row[q]).
+ */
+int tv_bias_from_ancestor_words(const uint64_t* words, int32_t words_per_row,
+                                const int32_t* query_to_request, const int32_t* query_local_row,
+                                const int32_t* node_counts, const int64_t* qq_bias_offsets,
+                                int32_t total_queries, float* qq_bias, void* stream);
+
 typedef struct tv_tree_attention_args {
     /* q [Q, Hq, D]; head dim contiguous */
     const void* q;

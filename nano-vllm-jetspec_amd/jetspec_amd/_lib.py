@@ -45,6 +45,8 @@ EXPORTED_SYMBOLS = (
     "tv_rope_scatter",
     "tv_argmax_rows",
     "tv_tree_accept",
+    "tv_ancestor_words_from_parents",
+    "tv_bias_from_ancestor_words",
 )
 
 
@@ -153,6 +155,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_rope_scatter.argtypes = [POINTER(RopeScatterArgs), c_void_p]
     lib.tv_argmax_rows.restype = c_int32
     lib.tv_argmax_rows.argtypes = [c_void_p, c_int64, c_int64, c_int64, c_int32, c_void_p, c_void_p]
+    lib.tv_ancestor_words_from_parents.restype = c_int32
+    lib.tv_ancestor_words_from_parents.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                                   c_void_p]
+    lib.tv_bias_from_ancestor_words.restype = c_int32
+    lib.tv_bias_from_ancestor_words.argtypes = [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
+                                                c_void_p, c_void_p]
     lib.tv_tree_accept.restype = c_int32
     lib.tv_tree_accept.argtypes = [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_int32, c_void_p,
                                    c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]

@@ -100,6 +100,10 @@ def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
     lib = _lib.library()
     device = metadata.tree_slots.device
     words = per_meta.get("ancestor_words")
+    prebuilt = getattr(metadata, "ancestor_words", None)
+    if words is None and prebuilt is not None:
+        per_meta["ancestor_words"] = words = prebuilt
+        per_meta["words_per_row"] = int(prebuilt.shape[1])
     if words is None:
         count = max(metadata.node_counts_host)
         per_row = (count + 63) // 64
