@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define TV_ABI_VERSION 1
+#define TV_ABI_VERSION 2
 
 enum tv_error {
     TV_OK = 0,
@@ -222,6 +222,30 @@ int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_
                            tv_attention_plan_info* info);
 
 /*
+ * Device-side planner: the same items and groups as tv_tree_attention_plan, item for
+ * item, computed on the device from device prefix_lens / node_counts, so a launch
+ * sequence keeps fixed grids while prefix lengths change (HIP graph replay, the
+ * equivalent of target_graph.py:95-167 reading live metadata).  No counterpart kernel
+ * in the reference: its Triton kernels read prefix lengths in every program.
+ * tv_tree_attention_plan_capacity gives capacities that hold for any prefix length up
+ * to max_prefix with these node counts (items <= CUs + sum of node-block groups x
+ * (1 + chunks forced by the LDS page cache), or groups x ceil(max_prefix / chunk_keys)
+ * for a forced chunk length), and the workspace those need.
+ * tv_tree_attention_plan_device writes items [item_capacity, 8], groups
+ * [group_capacity, 8] and counts[4] = {items, groups, partial slots, error}; on overflow
+ * it writes zero counts and error 1 instead of overrunning the arrays.
+ */
+int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, int32_t num_requests,
+                                    int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
+                                    int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info);
+
+int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* node_counts,
+                                  int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                  int32_t num_compute_units, int32_t chunk_keys, int32_t item_capacity,
+                                  int32_t group_capacity, int32_t slot_capacity, int32_t* items,
+                                  int32_t* groups, int32_t* counts, void* stream);
+
+/*
  * Packs the request-local additive ancestor bias of PackedTreeMetadata
  * (qq_bias f32, 0 = visible / -inf = hidden, row-major [local_q * T + node] at
  * qq_bias_offsets[r]; packed_metadata.py:93-100) into one bit per (row, node):
@@ -295,6 +319,10 @@ typedef struct tv_tree_attention_args {
     void* workspace;
     int64_t workspace_bytes;
     int32_t* status;                     /* optional */
+    /* optional: counts written by tv_tree_attention_plan_device ({items, groups, slots, error}).
+     * When set, num_items / num_groups / num_partial_slots are launch capacities and the
+     * kernels read the live counts from here (a graph-capturable launch). */
+    const int32_t* device_counts;
 } tv_tree_attention_args;
 
 /*

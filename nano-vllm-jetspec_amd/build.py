@@ -20,7 +20,7 @@ CSRC = HERE / "csrc"
 OUTPUT = HERE / "jetspec_amd" / "libtreeverify.so"
 ARCH = "gfx950"
 
-SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", "tv_rope.hip", "tv_accept.hip", "tv_metadata.hip")
+SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", "tv_rope.hip", "tv_accept.hip", "tv_metadata.hip", "tv_plan_device.hip")
 
 # Packed-FP32 VALU instructions are kept out of the device code (they are not
 # needed: the hot loops are MFMA and single-precision VALU work).

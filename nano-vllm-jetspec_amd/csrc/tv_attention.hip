@@ -132,6 +132,7 @@ struct AttnParams {
     float c;  // softmax scale * log2(e)
     const int32_t* items;
     const int32_t* groups;
+    const int32_t* counts;   // device {items, groups, ...} of a device-built plan, or null
     float* ws_o;
     float2* ws_ml;
     int32_t* status;
@@ -704,6 +705,8 @@ template <typename T>
 __global__ void __launch_bounds__(kThreads)
 tree_attention_kernel(const AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+    // A device-built plan launches a capacity grid; workgroups past its item count exit.
+    if (p.counts && static_cast<int>(blockIdx.x) >= p.counts[0]) return;
     const int32_t* d = p.items + 8 * blockIdx.x;
     const Item it{d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7]};
     if (it.r < 0 || it.r >= p.num_requests) {
@@ -728,6 +731,7 @@ tree_attention_kernel(const AttnParams p) {
 template <typename T>
 __global__ void __launch_bounds__(256)
 merge_partials_kernel(const AttnParams p) {
+    if (p.counts && static_cast<int>(blockIdx.x) >= p.counts[1]) return;
     const int32_t* gr = p.groups + 8 * blockIdx.x;
     const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
     if (r < 0 || r >= p.num_requests) return;
@@ -909,6 +913,7 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
     p.c = a->scale * kLog2e;
     p.items = a->items;
     p.groups = a->groups;
+    p.counts = a->device_counts;
     p.ws_o = static_cast<float*>(a->workspace);
     p.ws_ml = a->workspace ? reinterpret_cast<float2*>(static_cast<char*>(a->workspace) + o_span) : nullptr;
     p.status = a->status;

@@ -1,0 +1,380 @@
+// Device-side work planner for the packed tree-verify attention, for gfx950.
+//
+// Produces the same items and merge groups as the host planner (tv_plan.cpp), item for
+// item, but from the prefix lengths and node counts in device memory.  A launch sequence
+// that reads its plan from the device keeps fixed grid sizes while the prefix lengths
+// change, which is what a captured HIP graph replays: the attention and merge kernels
+// are launched with a capacity grid and their surplus workgroups exit on the counts
+// this planner writes.
+//
+// One 1024-thread workgroup:
+//   1. per request: KV heads per group, node blocks, cost; the total cost (reduction);
+//   2. per request: prefix chunk length and count (the host formulas), item / group /
+//      slot counts, and their exclusive prefix sums (one scan);
+//   3. every item gets a 64-bit sort key = (~cost, request, head group, chunk, block),
+//      the host's comparator; a bitonic sort in LDS orders them longest first;
+//   4. the XCD placement of the host (64-item windows, multi-block groups first,
+//      column-major), then the items and groups are written out.
+// Capacity overflow writes zero counts and an error flag instead of writing past the
+// caller's arrays.
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "tv_internal.h"
+
+namespace tv {
+namespace {
+
+constexpr int kPlanThreads = 1024;
+constexpr int kMaxSortItems = 8192;      // LDS sort capacity (64 KiB of keys)
+constexpr int kMaxPlanRequests = 2048;
+constexpr int kMinChunkKeys = 64;
+constexpr int kMaxChunkPages = 512;
+constexpr int kXcds = 8;
+
+struct PlanArgs {
+    const int32_t* prefix_lens;
+    const int32_t* node_counts;
+    int32_t num_requests, num_kv_heads, block_size, compute_units, chunk_keys;
+    int32_t item_capacity, group_capacity, slot_capacity;
+    int32_t* items;      // [item_capacity, 8]
+    int32_t* groups;     // [group_capacity, 8]
+    int32_t* counts;     // [4]: items, groups, partial slots, error
+};
+
+__device__ __forceinline__ int heads_per_group(int nodes, int kv_heads) {
+    int h = nodes <= 32 ? 2 : 1;
+    while (h > 1 && h > kv_heads) h >>= 1;
+    return h;
+}
+
+__device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// Block-wide exclusive scan of one int per thread (kPlanThreads threads); returns the
+// thread's prefix and writes the total to *total.
+__device__ int64_t block_scan(int64_t v, int64_t* scratch, int64_t* total) {
+    const int t = threadIdx.x;
+    scratch[t] = v;
+    __syncthreads();
+    for (int off = 1; off < kPlanThreads; off <<= 1) {
+        const int64_t add = t >= off ? scratch[t - off] : 0;
+        __syncthreads();
+        scratch[t] += add;
+        __syncthreads();
+    }
+    const int64_t inclusive = scratch[t];
+    if (t == kPlanThreads - 1) *total = inclusive;
+    __syncthreads();
+    return inclusive - v;
+}
+
+__global__ void __launch_bounds__(kPlanThreads)
+plan_device_kernel(const PlanArgs a) {
+    __shared__ uint64_t keys[kMaxSortItems];
+    __shared__ int64_t scan[kPlanThreads];
+    __shared__ int64_t totals[4];
+    __shared__ int32_t req_chunk[kMaxPlanRequests], req_nchunks[kMaxPlanRequests];
+    __shared__ int32_t req_item_off[kMaxPlanRequests], req_group_off[kMaxPlanRequests], req_slot_off[kMaxPlanRequests];
+    __shared__ int shared_flag;
+    const int t = threadIdx.x;
+    const int R = a.num_requests;
+    const int B = a.block_size;
+
+    // 1. Costs and their total.
+    int64_t my_cost = 0;
+    bool bad = false;
+    for (int r = t; r < R; r += kPlanThreads) {
+        const int p = a.prefix_lens[r], n = a.node_counts[r];
+        if (p < 0 || n < 1 || n > 1024) {
+            bad = true;
+            continue;
+        }
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int npw = 64 / hpw;
+        const int64_t groups = (a.num_kv_heads + hpw - 1) / hpw;
+        const int64_t blocks = (n + npw - 1) / npw;
+        my_cost += groups * blocks * hpw * (static_cast<int64_t>(p) + n);
+    }
+    if (t == 0) shared_flag = 0;
+    __syncthreads();
+    if (bad) atomicOr(&shared_flag, 1);
+    const int64_t cost_before = block_scan(my_cost, scan, &totals[0]);
+    (void)cost_before;
+    const int64_t total_cost = totals[0];
+    const int64_t target = max(static_cast<int64_t>(kMinChunkKeys), total_cost / a.compute_units);
+    const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * B) / 32 * 32;
+
+    // 2. Chunking and per-request counts.  Requests are handled in contiguous runs per
+    // thread so that one scan yields request-ordered offsets.
+    const int per_thread = (R + kPlanThreads - 1) / kPlanThreads;
+    const int r0 = min(R, t * per_thread), r1 = min(R, r0 + per_thread);
+    int64_t my_items = 0, my_groups = 0, my_slots = 0;
+    for (int r = r0; r < r1; ++r) {
+        const int p = max(0, a.prefix_lens[r]);
+        const int n = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int npw = 64 / hpw;
+        const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
+        const int64_t NB = (n + npw - 1) / npw;
+        int64_t chunk;
+        if (a.chunk_keys > 0) {
+            chunk = a.chunk_keys;
+        } else {
+            chunk = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), target / hpw), 32), max_chunk);
+            const int64_t nc = p > 0 ? (p + chunk - 1) / chunk : 1;
+            chunk = round_up((p + nc - 1) / max<int64_t>(nc, 1), 32);
+            if (chunk < 32) chunk = 32;
+        }
+        const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
+        req_chunk[r] = static_cast<int32_t>(chunk);
+        req_nchunks[r] = static_cast<int32_t>(nchunks);
+        my_items += G * NB * nchunks;
+        if (nchunks > 1) {
+            my_groups += G * NB;
+            my_slots += G * NB * nchunks;
+        }
+    }
+    int64_t item_base = block_scan(my_items, scan, &totals[1]);
+    int64_t group_base = block_scan(my_groups, scan, &totals[2]);
+    int64_t slot_base = block_scan(my_slots, scan, &totals[3]);
+    for (int r = r0; r < r1; ++r) {
+        const int n = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
+        const int64_t NB = (n + 64 / hpw - 1) / (64 / hpw);
+        req_item_off[r] = static_cast<int32_t>(item_base);
+        req_group_off[r] = static_cast<int32_t>(group_base);
+        req_slot_off[r] = static_cast<int32_t>(slot_base);
+        item_base += G * NB * req_nchunks[r];
+        if (req_nchunks[r] > 1) {
+            group_base += G * NB;
+            slot_base += G * NB * req_nchunks[r];
+        }
+    }
+    __syncthreads();
+    const int64_t num_items = totals[1], num_groups = totals[2], num_slots = totals[3];
+    const bool overflow = shared_flag || num_items > a.item_capacity || num_items > kMaxSortItems ||
+                          num_groups > a.group_capacity || num_slots > a.slot_capacity || R > kMaxPlanRequests;
+    if (overflow) {
+        if (t == 0) {
+            a.counts[0] = 0;
+            a.counts[1] = 0;
+            a.counts[2] = 0;
+            a.counts[3] = 1;
+        }
+        return;
+    }
+
+    // 3. Sort keys: (~cost, request, head group, chunk, block), each item's secondary
+    // index being its rank in that (request, head group, chunk, block) enumeration.
+    int npow = 1;
+    while (npow < num_items) npow <<= 1;
+    for (int e = t; e < npow; e += kPlanThreads) keys[e] = ~0ull;
+    __syncthreads();
+    for (int r = r0; r < r1; ++r) {
+        const int p = max(0, a.prefix_lens[r]);
+        const int n = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int G = (a.num_kv_heads + hpw - 1) / hpw;
+        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int nc = req_nchunks[r];
+        const int64_t chunk = req_chunk[r];
+        for (int hg = 0; hg < G; ++hg) {
+            for (int c = 0; c < nc; ++c) {
+                const int64_t kb = min(static_cast<int64_t>(p), c * chunk), ke = min(static_cast<int64_t>(p), (c + 1) * chunk);
+                const int64_t cost = static_cast<int64_t>(hpw) * ((ke - kb) + (c == nc - 1 ? n : 0));
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int64_t idx = req_item_off[r] + (static_cast<int64_t>(hg) * nc + c) * NB + nb;
+                    keys[idx] = (static_cast<uint64_t>(0x7fffffffu - static_cast<uint32_t>(cost)) << 32) |
+                                static_cast<uint32_t>(idx);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int size = 2; size <= npow; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int e = t; e < npow; e += kPlanThreads) {
+                const int partner = e ^ stride;
+                if (partner > e) {
+                    const bool ascending = (e & size) == 0;
+                    const uint64_t x = keys[e], y = keys[partner];
+                    if ((x > y) == ascending) {
+                        keys[e] = y;
+                        keys[partner] = x;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    // Decode a sorted key back into its item (request found by the offsets).
+    auto decode = [&](int64_t sorted_pos, int32_t* out) {
+        const int64_t idx = static_cast<int64_t>(keys[sorted_pos] & 0xffffffffull);
+        int lo = 0, hi = R - 1;
+        while (lo < hi) {      // last request whose item offset is <= idx
+            const int mid = (lo + hi + 1) >> 1;
+            if (req_item_off[mid] <= idx) lo = mid; else hi = mid - 1;
+        }
+        const int r = lo;
+        const int p = max(0, a.prefix_lens[r]);
+        const int n = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int nc = req_nchunks[r];
+        const int64_t local = idx - req_item_off[r];
+        const int nb = static_cast<int>(local % NB);
+        const int64_t hc = local / NB;
+        const int c = static_cast<int>(hc % nc);
+        const int hg = static_cast<int>(hc / nc);
+        const int64_t chunk = req_chunk[r];
+        out[0] = r;
+        out[1] = hg * hpw;
+        out[2] = nb * (64 / hpw);
+        out[3] = static_cast<int32_t>(min(static_cast<int64_t>(p), c * chunk));
+        out[4] = static_cast<int32_t>(min(static_cast<int64_t>(p), (c + 1) * chunk));
+        out[5] = c == nc - 1 ? 1 : 0;
+        out[6] = nc > 1 ? req_slot_off[r] + (hg * NB + nb) * nc + c : -1;
+        out[7] = hpw;
+    };
+    // Stream identity (request, head group, chunk) of a sorted position.
+    auto stream_of = [&](int64_t sorted_pos) -> int64_t {
+        const int64_t idx = static_cast<int64_t>(keys[sorted_pos] & 0xffffffffull);
+        int lo = 0, hi = R - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (req_item_off[mid] <= idx) lo = mid; else hi = mid - 1;
+        }
+        const int n = max(1, min(1024, a.node_counts[lo]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        return (static_cast<int64_t>(lo) << 32) | ((idx - req_item_off[lo]) / NB);
+    };
+
+    // 4. XCD placement (tv_plan.cpp::place_for_xcds) and output.
+    if (t == 0) shared_flag = 0;
+    __syncthreads();
+    for (int64_t i = 1 + t; i < num_items; i += kPlanThreads) {
+        if (stream_of(i) == stream_of(i - 1)) atomicOr(&shared_flag, 1);
+    }
+    __syncthreads();
+    const bool shared = shared_flag != 0;
+    constexpr int kWindow = kXcds * kXcds;
+    const int64_t full = shared ? (num_items / kWindow) * kWindow : 0;
+    for (int64_t i = t; i < num_items; i += kPlanThreads) {
+        int64_t dest = i;
+        if (i < full) {
+            const int64_t w = i - i % kWindow;
+            const int k = static_cast<int>(i - w);
+            // Rank of item k in the window's "grouped first" order.
+            auto grouped = [&](int j) {
+                const int64_t s = stream_of(w + j);
+                return (j + 1 < kWindow && stream_of(w + j + 1) == s) || (j > 0 && stream_of(w + j - 1) == s);
+            };
+            const bool mine = grouped(k);
+            int rank = 0;
+            for (int j = 0; j < kWindow; ++j) {
+                if (j == k) continue;
+                const bool g = grouped(j);
+                if (mine ? (g && j < k) : (g || j < k)) ++rank;
+            }
+            dest = w + kXcds * (rank % kXcds) + rank / kXcds;
+        }
+        decode(i, a.items + dest * 8);
+    }
+    // Merge groups in (request, head group, block) order with their first partial slot.
+    for (int r = r0; r < r1; ++r) {
+        const int nc = req_nchunks[r];
+        if (nc < 2) continue;
+        const int n = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int G = (a.num_kv_heads + hpw - 1) / hpw;
+        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        for (int hg = 0; hg < G; ++hg) {
+            for (int nb = 0; nb < NB; ++nb) {
+                int32_t* gr = a.groups + static_cast<int64_t>(req_group_off[r] + hg * NB + nb) * 8;
+                gr[0] = r;
+                gr[1] = hg * hpw;
+                gr[2] = nb * (64 / hpw);
+                gr[3] = hpw;
+                gr[4] = req_slot_off[r] + (hg * NB + nb) * nc;
+                gr[5] = nc;
+                gr[6] = 0;
+                gr[7] = 0;
+            }
+        }
+    }
+    if (t == 0) {
+        a.counts[0] = static_cast<int32_t>(num_items);
+        a.counts[1] = static_cast<int32_t>(num_groups);
+        a.counts[2] = static_cast<int32_t>(num_slots);
+        a.counts[3] = 0;
+    }
+}
+
+}  // namespace
+}  // namespace tv
+
+using namespace tv;
+
+extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, int32_t num_requests,
+                                               int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
+                                               int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info) {
+    clear_error();
+    if (!node_counts_host || !info || num_requests < 1 || num_kv_heads < 1 || block_size < 32 || block_size % 32 ||
+        num_compute_units < 1 || max_prefix < 0 || chunk_keys < 0 || chunk_keys % 32) {
+        return fail(TV_ERR_INVALID, "plan_capacity: invalid arguments");
+    }
+    if (num_requests > kMaxPlanRequests) {
+        return fail(TV_ERR_UNSUPPORTED, "plan_capacity: at most %d requests", kMaxPlanRequests);
+    }
+    // items <= CUs + sum_r G_r NB_r (1 + ceil(P_max / longest chunk)): a chunk is at least
+    // total/CUs keys per unit of cost unless it is capped by the LDS page cache.
+    const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
+    const int64_t capped = (max_prefix + max_chunk - 1) / max_chunk;
+    int64_t blocks = 0;
+    int32_t max_nodes = 1;
+    for (int32_t r = 0; r < num_requests; ++r) {
+        const int32_t n = node_counts_host[r];
+        if (n < 1 || n > 1024) return fail(TV_ERR_UNSUPPORTED, "plan_capacity: request %d has %d nodes", r, n);
+        max_nodes = n > max_nodes ? n : max_nodes;
+        const int hpw = n <= 32 && num_kv_heads >= 2 ? 2 : 1;
+        const int npw = 64 / hpw;
+        blocks += static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((n + npw - 1) / npw);
+    }
+    // A forced chunk length gives every node-block group ceil(P / chunk) items.
+    const int64_t items = chunk_keys > 0 ? blocks * std::max<int64_t>(1, (max_prefix + chunk_keys - 1) / chunk_keys)
+                                         : num_compute_units + blocks * (1 + capped);
+    if (items > kMaxSortItems) {
+        return fail(TV_ERR_UNSUPPORTED, "plan_capacity: %lld items exceed the device planner's %d",
+                    static_cast<long long>(items), kMaxSortItems);
+    }
+    info->num_items = static_cast<int32_t>(items);
+    info->num_groups = static_cast<int32_t>(blocks);
+    info->num_partial_slots = static_cast<int32_t>(items);
+    info->ancestor_words_per_row = (max_nodes + 63) / 64;
+    info->workspace_bytes = (items * 256 * 128 * 4 + 255) / 256 * 256 + (items * 256 * 8 + 255) / 256 * 256;
+    return TV_OK;
+}
+
+extern "C" int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* node_counts,
+                                             int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                             int32_t num_compute_units, int32_t chunk_keys, int32_t item_capacity,
+                                             int32_t group_capacity, int32_t slot_capacity, int32_t* items,
+                                             int32_t* groups, int32_t* counts, void* stream) {
+    clear_error();
+    if (num_requests < 1 || num_requests > kMaxPlanRequests || num_kv_heads < 1 || block_size < 32 ||
+        block_size % 32 || num_compute_units < 1 || chunk_keys < 0 || chunk_keys % 32 || item_capacity < 1 ||
+        item_capacity > kMaxSortItems || group_capacity < 0 || slot_capacity < 0) {
+        return fail(TV_ERR_INVALID, "plan_device: invalid arguments");
+    }
+    if (!prefix_lens || !node_counts || !items || !counts || (group_capacity > 0 && !groups)) {
+        return fail(TV_ERR_INVALID, "plan_device: null pointer");
+    }
+    PlanArgs a{prefix_lens, node_counts, num_requests, num_kv_heads, block_size, num_compute_units, chunk_keys,
+               item_capacity, group_capacity, slot_capacity, items, groups, counts};
+    hipLaunchKernelGGL(plan_device_kernel, dim3(1), dim3(kPlanThreads), 0, as_stream(stream), a);
+    return check_launch("plan_device");
+}

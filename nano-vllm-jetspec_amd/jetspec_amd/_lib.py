@@ -12,7 +12,7 @@ from pathlib import Path
 import threading
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libtreeverify.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TV_OK = 0
 TV_ERR_INVALID = -1
@@ -47,6 +47,8 @@ EXPORTED_SYMBOLS = (
     "tv_tree_accept",
     "tv_ancestor_words_from_parents",
     "tv_bias_from_ancestor_words",
+    "tv_tree_attention_plan_capacity",
+    "tv_tree_attention_plan_device",
 )
 
 
@@ -98,6 +100,7 @@ class TreeAttentionArgs(ctypes.Structure):
         ("workspace", c_void_p),
         ("workspace_bytes", c_int64),
         ("status", c_void_p),
+        ("device_counts", c_void_p),
     ]
 
 
@@ -161,6 +164,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_bias_from_ancestor_words.restype = c_int32
     lib.tv_bias_from_ancestor_words.argtypes = [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int32,
                                                 c_void_p, c_void_p]
+    lib.tv_tree_attention_plan_capacity.restype = c_int32
+    lib.tv_tree_attention_plan_capacity.argtypes = [POINTER(c_int32), c_int32, c_int32, c_int32, c_int32, c_int32,
+                                                    c_int64, POINTER(PlanInfo)]
+    lib.tv_tree_attention_plan_device.restype = c_int32
+    lib.tv_tree_attention_plan_device.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                                  c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]
     lib.tv_tree_accept.restype = c_int32
     lib.tv_tree_accept.argtypes = [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_int32, c_void_p,
                                    c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
