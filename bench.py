@@ -51,6 +51,9 @@ def parse_args():
     parser.add_argument("--cpu-requests", type=int, default=16,
                         help="requests of the batch timed on the CPU path (0 disables the CPU baseline)")
     parser.add_argument("--seed", type=int, default=None)
+    parser.add_argument("--legs", choices=("all", "verify"), default="all",
+                        help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
+                             "launches); 'all' adds the rope_scatter, accept and graph legs")
     return parser.parse_args()
 
 
@@ -334,9 +337,10 @@ def run_verify(args, torch):
                      "achieved_tflops": batch.algorithmic_flops() / (attn_ms * 1e-3) / 1e12,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
     }
-    result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
-    result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
-    result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
+    if args.legs == "all":
+        result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
+        result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
+        result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
     probe = copy_probe(torch)
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]

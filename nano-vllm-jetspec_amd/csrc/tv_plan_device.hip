@@ -76,6 +76,7 @@ plan_device_kernel(const PlanArgs a) {
     __shared__ int64_t totals[4];
     __shared__ int32_t req_chunk[kMaxPlanRequests], req_nchunks[kMaxPlanRequests];
     __shared__ int32_t req_item_off[kMaxPlanRequests], req_group_off[kMaxPlanRequests], req_slot_off[kMaxPlanRequests];
+    __shared__ int32_t stream_id[kMaxSortItems];   // (request, head group, chunk) of each sorted item
     __shared__ int shared_flag;
     const int t = threadIdx.x;
     const int R = a.num_requests;
@@ -254,10 +255,14 @@ plan_device_kernel(const PlanArgs a) {
     };
 
     // 4. XCD placement (tv_plan.cpp::place_for_xcds) and output.
+    for (int64_t i = t; i < num_items; i += kPlanThreads) {
+        const int64_t s = stream_of(i);
+        stream_id[i] = static_cast<int32_t>((s >> 32) * kMaxSortItems + (s & 0xffffffff));
+    }
     if (t == 0) shared_flag = 0;
     __syncthreads();
     for (int64_t i = 1 + t; i < num_items; i += kPlanThreads) {
-        if (stream_of(i) == stream_of(i - 1)) atomicOr(&shared_flag, 1);
+        if (stream_id[i] == stream_id[i - 1]) atomicOr(&shared_flag, 1);
     }
     __syncthreads();
     const bool shared = shared_flag != 0;
@@ -270,8 +275,8 @@ plan_device_kernel(const PlanArgs a) {
             const int k = static_cast<int>(i - w);
             // Rank of item k in the window's "grouped first" order.
             auto grouped = [&](int j) {
-                const int64_t s = stream_of(w + j);
-                return (j + 1 < kWindow && stream_of(w + j + 1) == s) || (j > 0 && stream_of(w + j - 1) == s);
+                const int32_t s = stream_id[w + j];
+                return (j + 1 < kWindow && stream_id[w + j + 1] == s) || (j > 0 && stream_id[w + j - 1] == s);
             };
             const bool mine = grouped(k);
             int rank = 0;
