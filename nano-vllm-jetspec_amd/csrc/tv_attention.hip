@@ -406,18 +406,32 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             dmask = static_cast<uint32_t>(tt - ntp) * 4;
         }
     };
-    auto lds_stage = [&](int offset) {
-        return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds + offset)));
+    // LDS destination of a DMA: this wave's part of the ring (one SGPR for tiles, one
+    // for ancestor words) plus a compile-time stage offset.  The empty asm makes the
+    // base opaque at each use, so the compiler emits one scalar add per DMA instead of
+    // keeping every stage address live (and spilled).
+    const uint32_t lds_base = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+    const uint32_t wave_tile_lds = lds_base + wave * 1024;
+    const uint32_t wave_mask_lds = lds_base + M_REGION + wave * 256;
+    auto tile_dst = [&](int offset) {
+        uint32_t base = wave_tile_lds;
+        asm volatile("" : "+s"(base));
+        return base + static_cast<uint32_t>(offset);
+    };
+    auto mask_dst = [&](int offset) {
+        uint32_t base = wave_mask_lds;
+        asm volatile("" : "+s"(base));
+        return base + static_cast<uint32_t>(offset);
     };
     auto issue_k = [&](int stage, int j) {
-        dma_b128(reinterpret_cast<const void*>(dk + k_hstep_b[j]), lds_stage(stage * TILE_SET + wave * 1024 + j * kTileBytes));
+        dma_b128(reinterpret_cast<const void*>(dk + k_hstep_b[j]), tile_dst(stage * TILE_SET + j * kTileBytes));
     };
     auto issue_v = [&](int stage, int j) {
         dma_b128(reinterpret_cast<const void*>(dv + v_hstep_b[j]),
-                 lds_stage(V_REGION + stage * TILE_SET + wave * 1024 + j * kTileBytes));
+                 tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
     };
     auto issue_mask = [&](int stage) {
-        if (dtree) dma_b32_s(m_lane_b, uniform_ptr(anc_req + dmask), lds_stage(M_REGION + stage * kMaskBytes + wave * 256));
+        if (dtree) dma_b32_s(m_lane_b, uniform_ptr(anc_req + dmask), mask_dst(stage * kMaskBytes));
     };
     auto issue_all = [&](int stage) {
 #pragma unroll
@@ -596,7 +610,56 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         describe(b, fetch(b));
         issue_all(b);
     }
-    int pf = fetch(NS - 2);
+
+    // Streaming DMA of whole prefix tiles.  Steps t < t_fast need no mask and stage a
+    // whole prefix tile t+NS-2, so their loads come from wave-uniform K and V tile
+    // bases (SGPRs) that advance by one tile per step, plus each lane's fixed byte
+    // offset; a new page is read from the LDS page list, prefetched one page ahead,
+    // when the current one is used up.  Pages hold whole tiles when B is a multiple
+    // of the tile (the item's first key is).
+    const int t_fast = (B % kTileKeys == 0) ? max(0, nfull - (NS - 2)) : 0;
+    uint64_t fk = 0, fv = 0;     // K and V base of the next streamed tile (head h0)
+    int f_left = 0, f_pidx = 0;  // tiles left in its page; the page's index in `pages`
+    int32_t f_next = 0;          // page number at f_pidx + 1
+    const uint32_t k_tile_b = kTileKeys * k_key_b, v_tile_b = kTileKeys * v_key_b;
+    const uint64_t k_head_u = reinterpret_cast<uint64_t>(uniform_ptr(reinterpret_cast<const void*>(k_head_b)));
+    const uint64_t v_head_u = reinterpret_cast<uint64_t>(uniform_ptr(reinterpret_cast<const void*>(v_head_b)));
+    uint32_t k_lane_h[HPW], v_lane_h[HPW];
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+        k_lane_h[j] = k_lane_b + static_cast<uint32_t>(k_hstep_b[j]);
+        v_lane_h[j] = v_lane_b + static_cast<uint32_t>(v_hstep_b[j]);
+    }
+    if (t_fast > 0) {
+        const uint32_t tile_pos = static_cast<uint32_t>(it.kbeg + kTileKeys * (NS - 2));
+        const uint32_t page_abs = pow2 ? (tile_pos >> bshift) : (tile_pos / static_cast<uint32_t>(B));
+        const uint32_t off0 = tile_pos - page_abs * static_cast<uint32_t>(B);
+        f_pidx = static_cast<int>(page_abs) - page0;
+        f_left = static_cast<int>((static_cast<uint32_t>(B) - off0) / kTileKeys);
+        const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(pages[f_pidx]));
+        fk = k_head_u + static_cast<uint64_t>(page) * k_page_b + static_cast<uint64_t>(off0) * k_key_b;
+        fv = v_head_u + static_cast<uint64_t>(page) * v_page_b + static_cast<uint64_t>(off0) * v_key_b;
+        f_next = pages[min(f_pidx + 1, npages - 1)];
+    }
+    auto fast_issue_k = [&](int stage, int j) {
+        dma_b128_s(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * kTileBytes));
+    };
+    auto fast_issue_v = [&](int stage, int j) {
+        dma_b128_s(v_lane_h[j], reinterpret_cast<const void*>(fv),
+                   tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+    };
+    auto fast_advance = [&]() {
+        fk += k_tile_b;
+        fv += v_tile_b;
+        if (--f_left == 0) {
+            const uint32_t page = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(f_next));
+            ++f_pidx;
+            f_next = pages[min(f_pidx + 1, npages - 1)];
+            fk = k_head_u + static_cast<uint64_t>(page) * k_page_b;
+            fv = v_head_u + static_cast<uint64_t>(page) * v_page_b;
+            f_left = B / kTileKeys;
+        }
+    };
     wait_vmcnt<(NS - 3) * LPT>();
     __syncthreads();
     f32x16 s = f32x16{};
@@ -612,10 +675,72 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         if (nfull == 0) mask_tile(s, 0, 0);
         raise_max(s, true);
     }
-    for (int t0 = 0; t0 < nt; t0 += NS) {
+    // Fast steps.  Active waves alternate two register sets for the scores and the
+    // probabilities by tile parity (NS is even, so the parity of t is that of b), so no
+    // copies between steps; inactive waves only stage their share of the tiles.
+    if (wave_active) {
+        f32x16 sc[2];
+        V8 pp[2][2];
+        sc[0] = s;
+        pp[0][0] = pb_prev[0];
+        pp[0][1] = pb_prev[1];
+        for (int t0 = 0; t0 < t_fast; t0 += NS) {
+#pragma unroll
+            for (int b = 0; b < NS; ++b) {
+                const int t = t0 + b;
+                if (t >= t_fast) break;
+                wait_vmcnt<(NS - 4) * LPT>();
+                __syncthreads();
+                const int ds = (b + NS - 2) % NS;
+                auto piece = [&](int sl) {
+                    if (HPW == 1) {
+                        if (sl == 4) fast_issue_k(ds, 0);
+                        if (sl == 8) fast_issue_v(ds, 0);
+                    } else {
+                        if (sl == 3 || sl == 5) fast_issue_k(ds, (sl - 3) >> 1);
+                        if (sl == 7 || sl == 9) fast_issue_v(ds, (sl - 7) >> 1);
+                    }
+                    if (sl == 12) fast_advance();
+                };
+                f32x16& s_cur = sc[b & 1];
+                float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], ((b + 1) % NS) * TILE_SET,
+                                ((b + NS - 1) % NS) * TILE_SET, piece);
+                const bool need = !(lt <= kMaxTileSum);
+                if (__any(need)) {
+                    raise_max(s_cur, need);
+                    lt = probabilities(s_cur, pp[(b + 1) & 1]);
+                }
+                l_run += lt;
+            }
+        }
+        const bool odd = t_fast & 1;
+        s = odd ? sc[1] : sc[0];
+        pb_prev[0] = odd ? pp[1][0] : pp[0][0];
+        pb_prev[1] = odd ? pp[1][1] : pp[0][1];
+    } else {
+        for (int t0 = 0; t0 < t_fast; t0 += NS) {
+#pragma unroll
+            for (int b = 0; b < NS; ++b) {
+                const int t = t0 + b;
+                if (t >= t_fast) break;
+                wait_vmcnt<(NS - 4) * LPT>();
+                __syncthreads();
+                const int ds = (b + NS - 2) % NS;
+#pragma unroll
+                for (int j = 0; j < HPW; ++j) fast_issue_k(ds, j);
+#pragma unroll
+                for (int j = 0; j < HPW; ++j) fast_issue_v(ds, j);
+                fast_advance();
+            }
+        }
+    }
+    // The remaining steps: masks, partial and tree tiles, general DMA.
+    int pf = fetch(t_fast + NS - 2);
+    for (int t0 = t_fast - t_fast % NS; t0 < nt; t0 += NS) {
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
             const int t = t0 + b;
+            if (t < t_fast) continue;
             if (t >= nt) break;
             wait_vmcnt<(NS - 4) * LPT>();
             __syncthreads();
