@@ -16,7 +16,9 @@ Prints ONE JSON line.  `value` = query rows (tree tokens) verified per second.
 (K/V of every visible position once per request and KV head + Q + O) over its mean
 duration from HIP events on the launch stream.  `cpu_baseline` times the reference's
 PyTorch CPU path (oracle/cpu_path.py) on a bounded sample of the same batch.
-Other configs (--config 1/2/3/5) are for measurement only.
+Other configs (--config 1/2/3/5) are for measurement only.  `--kv-heads 1` measures one
+tensor-parallel shard of the same batch (1 of the 8 KV heads with its 4 query heads, every
+request's full context): the share of one GPU in an 8-way split over KV heads.
 """
 from __future__ import annotations
 
@@ -51,6 +53,9 @@ def parse_args():
     parser.add_argument("--cpu-requests", type=int, default=16,
                         help="requests of the batch timed on the CPU path (0 disables the CPU baseline)")
     parser.add_argument("--seed", type=int, default=None)
+    parser.add_argument("--kv-heads", type=int, default=8, choices=(1, 2, 4, 8),
+                        help="KV heads of the batch (4 query heads each); below 8 it is one tensor-parallel "
+                             "shard, measured on the verify step only")
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
                              "launches); 'all' adds the rope_scatter, accept and graph legs")
@@ -288,6 +293,8 @@ def run_verify(args, torch):
 
     builder = {1: workloads.config1, 2: workloads.config2, 4: workloads.config4, 5: workloads.config5}[args.config]
     kwargs = {} if args.seed is None else {"seed": args.seed}
+    if args.kv_heads != 8:
+        kwargs["kv_heads"] = args.kv_heads
     batch = builder("cuda", **kwargs)
     meta = batch.metadata
     stream = torch.cuda.current_stream()
@@ -328,16 +335,19 @@ def run_verify(args, torch):
         "data": "synthetic (seeded N(0,1) bf16 Q/K/V, seeded parent arrays, permuted page pool)",
         "config": {"workload": WORKLOADS[args.config], "requests": meta.num_requests,
                    "tree_rows_per_step": tokens, "prefix_tokens": sum(meta.prefix_lengths),
-                   "q_heads": 32, "kv_heads": 8, "head_dim": 128, "page": meta.block_size, "layers_per_step": 1,
-                   "pool_pages": batch.info["pages"]},
+                   "q_heads": batch.q_heads, "kv_heads": batch.kv_heads, "head_dim": 128,
+                   "page": meta.block_size, "layers_per_step": 1, "pool_pages": batch.info["pages"]},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes(args.config),
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic_bytes(args.config) if args.kv_heads == 8 else None,
                      "kernel": "tree_attention_kernel", "kernel_ms": attn_ms, "algorithmic_bytes": algo_bytes,
                      "algorithmic_flops": batch.algorithmic_flops(),
                      "achieved_tflops": batch.algorithmic_flops() / (attn_ms * 1e-3) / 1e12,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
     }
-    if args.legs == "all":
+    if args.kv_heads != 8:
+        result["config"]["shard"] = f"tensor-parallel shard: {batch.kv_heads} of 8 KV heads"
+    if args.legs == "all" and args.kv_heads == 8:
         result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
         result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)

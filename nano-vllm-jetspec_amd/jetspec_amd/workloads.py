@@ -77,12 +77,20 @@ class VerifyBatch:
     def total_queries(self) -> int:
         return self.metadata.total_queries
 
+    @property
+    def kv_heads(self) -> int:
+        return self.k_pool.shape[2]
+
+    @property
+    def q_heads(self) -> int:
+        return self.q.shape[1]
+
     def algorithmic_bytes(self) -> int:
         """K/V of every visible position once per (request, KV head) + Q read + O write."""
         e = self.q.element_size()
-        kv = sum(2 * (p + t) * KV_HEADS * HEAD_DIM * e
+        kv = sum(2 * (p + t) * self.kv_heads * HEAD_DIM * e
                  for p, t in zip(self.metadata.prefix_lengths, self.metadata.node_counts_host))
-        qo = 2 * self.total_queries * Q_HEADS * HEAD_DIM * e
+        qo = 2 * self.total_queries * self.q_heads * HEAD_DIM * e
         return kv + qo
 
     def algorithmic_flops(self) -> int:
@@ -90,21 +98,22 @@ class VerifyBatch:
         total = 0
         for prefix, parents in zip(self.metadata.prefix_lengths, self.parents):
             visible = sum(prefix + d + 1 for d in depths_of(parents))
-            total += 4 * Q_HEADS * HEAD_DIM * visible
+            total += 4 * self.q_heads * HEAD_DIM * visible
         return total
 
     def append_bytes(self) -> int:
-        return 2 * 2 * self.total_queries * KV_HEADS * HEAD_DIM * self.new_k.element_size()
+        return 2 * 2 * self.total_queries * self.kv_heads * HEAD_DIM * self.new_k.element_size()
 
 
 def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: torch.device | str,
                        seed: int, dtype: torch.dtype = torch.bfloat16, pool_fill: float = 1.0,
-                       poison: bool = True, name: str = "") -> VerifyBatch:
+                       poison: bool = True, name: str = "", kv_heads: int = KV_HEADS) -> VerifyBatch:
     """Pages and slots from a permuted pool; payloads N(0,1); unused rows NaN if `poison`.
 
     `pool_fill` < 1 sizes the pool so live pages fill that fraction (fragmentation).
     Tree K/V are written into their scratch slots (the post-append state) and also
-    returned as `new_k`/`new_v` for timing the append.
+    returned as `new_k`/`new_v` for timing the append.  `kv_heads` < 8 builds one
+    tensor-parallel shard: that many KV heads and 4 query heads per KV head.
     """
     device = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -131,7 +140,8 @@ def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: t
         offset += n
     metadata = PackedTreeMetadata.build(prefixes, tables, slots, masks, BLOCK)
     gen = torch.Generator(device=device).manual_seed(seed)
-    shape = (total_pages, BLOCK, KV_HEADS, HEAD_DIM)
+    groups = Q_HEADS // KV_HEADS
+    shape = (total_pages, BLOCK, kv_heads, HEAD_DIM)
     k_pool = torch.empty(shape, dtype=dtype, device=device)
     v_pool = torch.empty(shape, dtype=dtype, device=device)
     k_pool.normal_(generator=gen)
@@ -143,15 +153,16 @@ def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: t
             used[np.asarray(table, dtype=np.int64)[pos // BLOCK] * BLOCK + pos % BLOCK] = True
         used[np.asarray(metadata.tree_slot_ids, dtype=np.int64)] = True
         unused = torch.as_tensor(np.flatnonzero(~used), device=device)
-        k_pool.view(-1, KV_HEADS, HEAD_DIM)[unused] = float("nan")
-        v_pool.view(-1, KV_HEADS, HEAD_DIM)[unused] = float("nan")
+        k_pool.view(-1, kv_heads, HEAD_DIM)[unused] = float("nan")
+        v_pool.view(-1, kv_heads, HEAD_DIM)[unused] = float("nan")
     total_q = metadata.total_queries
-    q = torch.randn((total_q, Q_HEADS, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
-    new_k = torch.randn((total_q, KV_HEADS, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
-    new_v = torch.randn((total_q, KV_HEADS, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
+    q = torch.randn((total_q, groups * kv_heads, HEAD_DIM), generator=gen, device=device,
+                    dtype=torch.float32).to(dtype)
+    new_k = torch.randn((total_q, kv_heads, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
+    new_v = torch.randn((total_q, kv_heads, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
     tree_slots = metadata.tree_slots
-    k_pool.view(-1, KV_HEADS, HEAD_DIM)[tree_slots] = new_k
-    v_pool.view(-1, KV_HEADS, HEAD_DIM)[tree_slots] = new_v
+    k_pool.view(-1, kv_heads, HEAD_DIM)[tree_slots] = new_k
+    v_pool.view(-1, kv_heads, HEAD_DIM)[tree_slots] = new_v
     return VerifyBatch(q=q, k_pool=k_pool, v_pool=v_pool, metadata=metadata, new_k=new_k, new_v=new_v,
                        parents=[list(p) for p in trees], prefix_pages=tables, name=name,
                        info={"pages": total_pages, "pool_fill": pool_fill, "seed": seed})
