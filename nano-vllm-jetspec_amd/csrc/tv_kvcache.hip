@@ -53,8 +53,12 @@ store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
 //   1. commit_check:   per 256 destinations, OR of {overlap with any source,
 //                      out-of-range slot}; one flag word per workgroup, always
 //                      written, so the workspace needs no clearing.
-//   2. commit_copy:    no flag -> direct copy; overlap -> gather into workspace.
-//   3. commit_scatter: overlap -> scatter workspace to destinations; else exits.
+//   2. commit_move:    no flag -> every workgroup copies its rows of one (K/V,
+//                      layer) plane directly, all of a thread's loads in flight
+//                      before its stores; overlap alone -> workgroup 0 gathers
+//                      every row into the workspace, synchronises, and scatters
+//                      them (the reference's order; never taken by the served
+//                      callers); an invalid slot -> nothing is written.
 
 constexpr int kCheckThreads = 256;
 constexpr int kSrcTile = 1024;
@@ -119,45 +123,71 @@ __device__ __forceinline__ char* slot_row(const PoolGeom& g, int64_t kv, int64_t
     return g.base + kv * g.s_kv + layer * g.s_layer + block * g.s_block + off * g.s_off;
 }
 
-// mode 0: direct src -> dst (only when no flag is set)
-// mode 1: gather src -> workspace (only when the overlap flag alone is set)
-// mode 2: scatter workspace -> dst (only when the overlap flag alone is set)
-template <typename Unit, int kMode>
-__global__ void __launch_bounds__(256)
+constexpr int kMoveRows = 8;        // slot rows of one plane per workgroup
+constexpr int kMoveThreads = 256;
+constexpr int kMoveUnroll = 8;      // units a thread keeps in flight (16 B each at most)
+
+// Byte offset of `slot`'s row within a (K/V, layer) plane.
+__device__ __forceinline__ int64_t slot_offset(const PoolGeom& g, int64_t slot) {
+    const int64_t block = slot / g.block_size;
+    const int64_t off = slot - block * g.block_size;
+    return block * g.s_block + off * g.s_off;
+}
+
+// Grid (ceil(n / kMoveRows), 2 * layers).  Runs after commit_check on the same stream.
+template <typename Unit>
+__global__ void __launch_bounds__(kMoveThreads)
 commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
-                   const int32_t* __restrict__ flags, int32_t num_flags,
-                   Unit* __restrict__ staging) {
+                   const int32_t* __restrict__ flags, int32_t num_flags, Unit* __restrict__ staging) {
     const int32_t f = read_flags(flags, num_flags);
-    if (kMode == 0 && f != 0) return;
-    if (kMode != 0 && f != kFlagOverlap) return;
-    const int64_t rows = 2 * g.layers * g.n;
+    if (f & kFlagInvalid) return;
     const int32_t upr = g.units_per_row;
-    // Each iteration a workgroup moves `rows_per_iter` rows; a thread owns one
-    // unit of one row, so all loads of the iteration are in flight together.
-    const int32_t rows_per_iter = upr >= 256 ? 1 : 256 / upr;
-    const int32_t sub = upr >= 256 ? 0 : threadIdx.x / upr;
-    const int32_t lane_unit = upr >= 256 ? threadIdx.x : threadIdx.x % upr;
-    if (sub >= rows_per_iter) return;
-    for (int64_t row0 = static_cast<int64_t>(blockIdx.x) * rows_per_iter; row0 < rows;
-         row0 += static_cast<int64_t>(gridDim.x) * rows_per_iter) {
-        const int64_t row = row0 + sub;
-        if (row >= rows) break;
-        const int64_t i = row % g.n;
-        const int64_t kl = row / g.n;
-        const int64_t layer = kl % g.layers;
-        const int64_t kv = kl / g.layers;
-        if (kMode == 0) {
-            const Unit* s = reinterpret_cast<const Unit*>(slot_row(g, kv, layer, src[i]));
-            Unit* d = reinterpret_cast<Unit*>(slot_row(g, kv, layer, dst[i]));
-            for (int32_t u = lane_unit; u < upr; u += 256) d[u] = s[u];
-        } else if (kMode == 1) {
-            const Unit* s = reinterpret_cast<const Unit*>(slot_row(g, kv, layer, src[i]));
-            Unit* d = staging + row * upr;
-            for (int32_t u = lane_unit; u < upr; u += 256) d[u] = s[u];
-        } else {
-            const Unit* s = staging + row * upr;
-            Unit* d = reinterpret_cast<Unit*>(slot_row(g, kv, layer, dst[i]));
-            for (int32_t u = lane_unit; u < upr; u += 256) d[u] = s[u];
+    if (f == kFlagOverlap) {
+        // Gather every row into the workspace, then scatter: one workgroup, so the
+        // barrier orders all reads before all writes.
+        if (blockIdx.x != 0 || blockIdx.y != 0) return;
+        const int64_t rows = 2 * g.layers * g.n;
+        for (int64_t u = threadIdx.x; u < rows * upr; u += kMoveThreads) {
+            const int64_t row = u / upr, i = row % g.n, plane = row / g.n;
+            const char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+            staging[u] = reinterpret_cast<const Unit*>(base + slot_offset(g, src[i]))[u % upr];
+        }
+        __syncthreads();
+        for (int64_t u = threadIdx.x; u < rows * upr; u += kMoveThreads) {
+            const int64_t row = u / upr, i = row % g.n, plane = row / g.n;
+            char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+            reinterpret_cast<Unit*>(base + slot_offset(g, dst[i]))[u % upr] = staging[u];
+        }
+        return;
+    }
+    __shared__ int64_t row_src[kMoveRows], row_dst[kMoveRows];
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kMoveRows;
+    const int32_t nrows = static_cast<int32_t>(g.n - i0 < kMoveRows ? g.n - i0 : kMoveRows);
+    const int32_t plane = blockIdx.y;
+    char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+    if (threadIdx.x < nrows) {
+        row_src[threadIdx.x] = slot_offset(g, src[i0 + threadIdx.x]);
+        row_dst[threadIdx.x] = slot_offset(g, dst[i0 + threadIdx.x]);
+    }
+    __syncthreads();
+    const int32_t total = nrows * upr;
+    for (int32_t u0 = 0; u0 < total; u0 += kMoveThreads * kMoveUnroll) {
+        Unit v[kMoveUnroll];
+#pragma unroll
+        for (int k = 0; k < kMoveUnroll; ++k) {
+            const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
+            if (u < total) {
+                const int32_t r = u / upr, c = u - r * upr;
+                v[k] = reinterpret_cast<const Unit*>(base + row_src[r])[c];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kMoveUnroll; ++k) {
+            const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
+            if (u < total) {
+                const int32_t r = u / upr, c = u - r * upr;
+                reinterpret_cast<Unit*>(base + row_dst[r])[c] = v[k];
+            }
         }
     }
 }
@@ -165,18 +195,14 @@ commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* _
 template <typename Unit>
 int launch_commit(const PoolGeom& g, const int64_t* src, const int64_t* dst, int32_t* flags,
                   int32_t num_flags, void* staging, hipStream_t stream) {
-    const int64_t rows = 2 * g.layers * g.n;
-    const int32_t rows_per_iter = g.units_per_row >= 256 ? 1 : 256 / g.units_per_row;
-    int64_t blocks = (rows + rows_per_iter - 1) / rows_per_iter;
-    if (blocks > 8192) blocks = 8192;
-    if (blocks < 1) blocks = 1;
-    Unit* st = static_cast<Unit*>(staging);
-    hipLaunchKernelGGL((commit_move_kernel<Unit, 0>), dim3(blocks), dim3(256), 0, stream, g, src, dst,
-                       flags, num_flags, st);
-    hipLaunchKernelGGL((commit_move_kernel<Unit, 1>), dim3(blocks), dim3(256), 0, stream, g, src, dst,
-                       flags, num_flags, st);
-    hipLaunchKernelGGL((commit_move_kernel<Unit, 2>), dim3(blocks), dim3(256), 0, stream, g, src, dst,
-                       flags, num_flags, st);
+    const int64_t groups = (g.n + kMoveRows - 1) / kMoveRows;
+    const int64_t planes = 2 * g.layers;
+    if (groups > 0x7fffffff || planes > 65535) {
+        return fail(TV_ERR_UNSUPPORTED, "copy_accepted_kv: %lld slots x %lld layers exceed the launch grid",
+                    (long long)g.n, (long long)g.layers);
+    }
+    hipLaunchKernelGGL((commit_move_kernel<Unit>), dim3(static_cast<uint32_t>(groups), static_cast<uint32_t>(planes)),
+                       dim3(kMoveThreads), 0, stream, g, src, dst, flags, num_flags, static_cast<Unit*>(staging));
     return check_launch("copy_accepted_kv");
 }
 
