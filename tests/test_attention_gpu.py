@@ -28,11 +28,11 @@ def heap_parents(n):
     return [-1] + [(i - 1) // 2 for i in range(1, n)]
 
 
-def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dtype=torch.bfloat16, seed=317):
+def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dtype=torch.bfloat16, seed=317,
+                      block=256):
     """The reference GPU fixture geometry (tests/test_jetspec_packed_attention.py:109-125) with
     shuffled pages, scattered scratch slots and NaN in every unused pool row."""
     rng = np.random.default_rng(seed)
-    block = 256
     prefix_pages = [-(-p // block) for p in prefixes]
     scratch_pages = -(-sum(counts) // block) + 1
     total = sum(prefix_pages) + scratch_pages + 3
@@ -80,6 +80,20 @@ def test_config1_all_rows_match_oracle():
 def test_reference_fixture_nan_poisoned_pool():
     q, k, v, meta, *_ = reference_fixture()
     check_all_rows(q, k, v, meta, "fixture(63,31,47)")
+
+
+@pytest.mark.parametrize("block", [32, 64, 96, 128, 512])
+@pytest.mark.parametrize("chunk", [0, 96, 480])
+def test_block_sizes_and_unaligned_chunks(block, chunk):
+    """Page sizes other than 256 and prefix chunks that start inside a page.  The kernel's
+    streaming loop moves to the next page every block/32 tiles (every tile at 32, from a
+    mid-page start when a chunk begins inside a page); 96 is not a power of two.  Every
+    unused pool row is NaN, so a wrong page or slot shows up."""
+    prefixes = (0, 31, 250, 1000, 2049, 4100)
+    counts = (16, 33, 64, 7, 64, 20)
+    q, k, v, meta, *_ = reference_fixture(prefixes, counts, kv_heads=2, seed=900 + block + chunk, block=block)
+    print(f"[blocks] block={block} chunk={chunk}", flush=True)
+    check_all_rows(q, k, v, meta, f"block {block} chunk {chunk}", chunk_keys=chunk)
 
 
 @pytest.mark.parametrize("prefix", [0, 1, 63, 64, 65, 255, 256, 257, 1024, 2048])
