@@ -59,6 +59,8 @@ store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
 //                      every row into the workspace, synchronises, and scatters
 //                      them (the reference's order; never taken by the served
 //                      callers); an invalid slot -> nothing is written.
+// Up to kFusedMaxSlots slots (every served round) take one launch instead,
+// commit_fused_kernel, which does the same per row without the flag pass.
 
 constexpr int kCheckThreads = 256;
 constexpr int kSrcTile = 1024;
@@ -134,6 +136,36 @@ __device__ __forceinline__ int64_t slot_offset(const PoolGeom& g, int64_t slot) 
     return block * g.s_block + off * g.s_off;
 }
 
+// Direct copy of up to kMoveRows rows of one (K/V, layer) plane whose byte offsets
+// within the plane are in LDS; rows whose bit is set in `skip` are left alone.  Every
+// thread issues up to kMoveUnroll loads before its stores.
+template <typename Unit>
+__device__ __forceinline__ void copy_rows(const PoolGeom& g, int32_t plane, const int64_t* row_src,
+                                          const int64_t* row_dst, int32_t nrows, uint32_t skip) {
+    char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+    const int32_t upr = g.units_per_row;
+    const int32_t total = nrows * upr;
+    for (int32_t u0 = 0; u0 < total; u0 += kMoveThreads * kMoveUnroll) {
+        Unit v[kMoveUnroll];
+#pragma unroll
+        for (int k = 0; k < kMoveUnroll; ++k) {
+            const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
+            if (u < total) {
+                const int32_t r = u / upr, c = u - r * upr;
+                if (!((skip >> r) & 1u)) v[k] = reinterpret_cast<const Unit*>(base + row_src[r])[c];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kMoveUnroll; ++k) {
+            const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
+            if (u < total) {
+                const int32_t r = u / upr, c = u - r * upr;
+                if (!((skip >> r) & 1u)) reinterpret_cast<Unit*>(base + row_dst[r])[c] = v[k];
+            }
+        }
+    }
+}
+
 // Grid (ceil(n / kMoveRows), 2 * layers).  Runs after commit_check on the same stream.
 template <typename Unit>
 __global__ void __launch_bounds__(kMoveThreads)
@@ -164,32 +196,103 @@ commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* _
     const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kMoveRows;
     const int32_t nrows = static_cast<int32_t>(g.n - i0 < kMoveRows ? g.n - i0 : kMoveRows);
     const int32_t plane = blockIdx.y;
-    char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
     if (threadIdx.x < nrows) {
         row_src[threadIdx.x] = slot_offset(g, src[i0 + threadIdx.x]);
         row_dst[threadIdx.x] = slot_offset(g, dst[i0 + threadIdx.x]);
     }
     __syncthreads();
-    const int32_t total = nrows * upr;
-    for (int32_t u0 = 0; u0 < total; u0 += kMoveThreads * kMoveUnroll) {
-        Unit v[kMoveUnroll];
-#pragma unroll
-        for (int k = 0; k < kMoveUnroll; ++k) {
-            const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
-            if (u < total) {
-                const int32_t r = u / upr, c = u - r * upr;
-                v[k] = reinterpret_cast<const Unit*>(base + row_src[r])[c];
-            }
+    copy_rows<Unit>(g, plane, row_src, row_dst, nrows, 0u);
+}
+
+// One-launch commit for up to kFusedMaxSlots slots.  Row i is "dirty" when its
+// source is some row's destination or its destination some row's source; a clean
+// row's source is never written and its destination never read by any row, so it
+// can be copied directly whatever the other rows do.  Workgroups (x >= 1, y) copy
+// the clean rows among rows 8(x-1)..8(x-1)+7 of plane y; workgroup (0, 0) finds the
+// dirty rows and moves them through the workspace (gather all, barrier, scatter
+// all), the reference's order.  Every workgroup validates every slot first, so an
+// invalid map writes nothing anywhere.
+constexpr int64_t kFusedMaxSlots = 2048;
+
+template <typename Unit>
+__global__ void __launch_bounds__(kMoveThreads)
+commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
+                    int64_t pool_slots, Unit* __restrict__ staging, int32_t* status) {
+    if (blockIdx.x == 0 && blockIdx.y != 0) return;
+    const int32_t n = static_cast<int32_t>(g.n);
+    if (blockIdx.x == 0) {
+        // The dirty-row mover: slot lists in LDS, every row's test against all of them.
+        __shared__ int64_t s_src[kFusedMaxSlots], s_dst[kFusedMaxSlots];
+        __shared__ uint8_t dirty[kFusedMaxSlots];
+        int bad = 0;
+        for (int32_t k = threadIdx.x; k < n; k += kMoveThreads) {
+            const int64_t a = src[k], b = dst[k];
+            s_src[k] = a;
+            s_dst[k] = b;
+            bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
         }
+        if (__syncthreads_or(bad)) {
+            if (threadIdx.x == 0) set_status(status, TV_STATUS_BAD_SLOT);
+            return;
+        }
+        int any = 0;
+        for (int32_t i = threadIdx.x; i < n; i += kMoveThreads) {
+            const int64_t a = s_src[i], b = s_dst[i];
+            int d = 0;
+            for (int32_t k = 0; k < n; ++k) d |= (a == s_dst[k]) | (b == s_src[k]);
+            dirty[i] = static_cast<uint8_t>(d);
+            any |= d;
+        }
+        if (!__syncthreads_or(any)) return;
+        const int32_t upr = g.units_per_row;
+        const int64_t rows = 2 * g.layers * g.n;
+        for (int64_t u = threadIdx.x; u < rows * upr; u += kMoveThreads) {
+            const int64_t row = u / upr, i = row % g.n, plane = row / g.n;
+            if (!dirty[i]) continue;
+            const char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+            staging[u] = reinterpret_cast<const Unit*>(base + slot_offset(g, s_src[i]))[u % upr];
+        }
+        __syncthreads();
+        for (int64_t u = threadIdx.x; u < rows * upr; u += kMoveThreads) {
+            const int64_t row = u / upr, i = row % g.n, plane = row / g.n;
+            if (!dirty[i]) continue;
+            char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+            reinterpret_cast<Unit*>(base + slot_offset(g, s_dst[i]))[u % upr] = staging[u];
+        }
+        return;
+    }
+    // Clean-row copier for rows i0..i0+nrows-1 of plane blockIdx.y.  Its own rows'
+    // slots and this thread's share of all slots are loaded together, so validity and
+    // dirtiness cost one round trip before the copy.
+    __shared__ int64_t row_src[kMoveRows], row_dst[kMoveRows];
+    __shared__ uint32_t skip;
+    const int32_t i0 = (blockIdx.x - 1) * kMoveRows;
+    const int32_t nrows = n - i0 < kMoveRows ? n - i0 : kMoveRows;
+    int64_t my_s[kMoveRows], my_d[kMoveRows];
 #pragma unroll
-        for (int k = 0; k < kMoveUnroll; ++k) {
-            const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
-            if (u < total) {
-                const int32_t r = u / upr, c = u - r * upr;
-                reinterpret_cast<Unit*>(base + row_dst[r])[c] = v[k];
-            }
+    for (int r = 0; r < kMoveRows; ++r) {
+        my_s[r] = r < nrows ? src[i0 + r] : -1;
+        my_d[r] = r < nrows ? dst[i0 + r] : -1;
+    }
+    if (threadIdx.x == 0) skip = 0u;
+    int bad = 0;
+    uint32_t mine = 0u;
+    for (int32_t k = threadIdx.x; k < n; k += kMoveThreads) {
+        const int64_t a = src[k], b = dst[k];
+        bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
+#pragma unroll
+        for (int r = 0; r < kMoveRows; ++r) {
+            if (r < nrows && (my_s[r] == b || my_d[r] == a)) mine |= 1u << r;
         }
     }
+    if (threadIdx.x < nrows) {
+        row_src[threadIdx.x] = slot_offset(g, my_s[threadIdx.x]);
+        row_dst[threadIdx.x] = slot_offset(g, my_d[threadIdx.x]);
+    }
+    __syncthreads();
+    if (mine) atomicOr(&skip, mine);
+    if (__syncthreads_or(bad)) return;
+    copy_rows<Unit>(g, blockIdx.y, row_src, row_dst, nrows, skip);
 }
 
 template <typename Unit>
@@ -349,9 +452,29 @@ extern "C" int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6], c
     const int64_t flag_bytes = ((static_cast<int64_t>(nflags) * 4 + 255) / 256) * 256;
     void* staging = static_cast<char*>(workspace) + flag_bytes;
     hipStream_t s = as_stream(stream);
+    int rc;
+    if (num_slots <= kFusedMaxSlots && 2 * layers <= 65535) {
+        const dim3 grid(static_cast<uint32_t>((num_slots + kMoveRows - 1) / kMoveRows + 1),
+                        static_cast<uint32_t>(2 * layers));
+        switch (unit) {
+            case 16: hipLaunchKernelGGL(commit_fused_kernel<u32x4>, grid, dim3(kMoveThreads), 0, s, g, source_slots,
+                                        destination_slots, pool_slots, static_cast<u32x4*>(staging), status); break;
+            case 8: hipLaunchKernelGGL(commit_fused_kernel<u32x2>, grid, dim3(kMoveThreads), 0, s, g, source_slots,
+                                       destination_slots, pool_slots, static_cast<u32x2*>(staging), status); break;
+            case 4: hipLaunchKernelGGL(commit_fused_kernel<uint32_t>, grid, dim3(kMoveThreads), 0, s, g, source_slots,
+                                       destination_slots, pool_slots, static_cast<uint32_t*>(staging), status); break;
+            case 2: hipLaunchKernelGGL(commit_fused_kernel<uint16_t>, grid, dim3(kMoveThreads), 0, s, g, source_slots,
+                                       destination_slots, pool_slots, static_cast<uint16_t*>(staging), status); break;
+            default: hipLaunchKernelGGL(commit_fused_kernel<uint8_t>, grid, dim3(kMoveThreads), 0, s, g, source_slots,
+                                        destination_slots, pool_slots, static_cast<uint8_t*>(staging), status); break;
+        }
+        rc = check_launch("copy_accepted_kv");
+        if (rc != TV_OK) return rc;
+        if (payload_bytes_host) *payload_bytes_host = payload;
+        return TV_OK;
+    }
     hipLaunchKernelGGL(commit_check_kernel, dim3(nflags), dim3(kCheckThreads), 0, s, source_slots,
                        destination_slots, num_slots, pool_slots, flags, status);
-    int rc;
     switch (unit) {
         case 16: rc = launch_commit<u32x4>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
         case 8: rc = launch_commit<u32x2>(g, source_slots, destination_slots, flags, nflags, staging, s); break;

@@ -71,25 +71,29 @@ def test_store_contract_assertions():
                       torch.zeros(4, dtype=torch.int64, device=DEV))
 
 
-def small_commit_case(seed, overlap=False, layers=4):
+def small_commit_case(seed, overlap=False, layers=4, rows=200, pages=12):
     rng = np.random.default_rng(seed)
-    pool = torch.randn((2, layers, 12, 256, 8, 128), generator=torch.Generator(device=DEV).manual_seed(seed),
+    pool = torch.randn((2, layers, pages, 256, 8, 128), generator=torch.Generator(device=DEV).manual_seed(seed),
                        device=DEV).to(torch.bfloat16)
-    slots = rng.permutation(12 * 256)
-    src, dst = slots[:200], slots[200:400]
+    slots = rng.permutation(pages * 256)
+    src, dst = slots[:rows], slots[rows:2 * rows]
     if overlap:
         dst = dst.copy()
-        dst[::3] = src[rng.permutation(200)[:len(dst[::3])]]
+        dst[::3] = src[rng.permutation(rows)[:len(dst[::3])]]
     return pool, src.astype(np.int64), dst.astype(np.int64)
 
 
+# 200 rows take the one-launch commit; 3000 rows (above its 2048-slot limit) the
+# check + move launches.
+@pytest.mark.parametrize("rows,layers,pages", [(200, 4, 12), (3000, 2, 24)])
 @pytest.mark.parametrize("overlap", [False, True])
-def test_commit_bit_exact_against_oracle(overlap):
-    pool, src, dst = small_commit_case(11, overlap)
+def test_commit_bit_exact_against_oracle(overlap, rows, layers, pages):
+    pool, src, dst = small_commit_case(11, overlap, layers=layers, rows=rows, pages=pages)
+    print(f"[commit] rows={rows} layers={layers} overlap={overlap}", flush=True)
     expect = as_bytes(pool).copy().view(np.uint16).reshape(pool.shape)
     payload = copy_accepted_kv(pool, torch.as_tensor(src, device=DEV), torch.as_tensor(dst, device=DEV), 256)
     torch.cuda.synchronize()
-    assert payload == 200 * 2 * 4 * 8 * 128 * 2
+    assert payload == rows * 2 * layers * 8 * 128 * 2
     assert oracle.copy_accepted_kv(expect, src, dst) == payload
     assert np.array_equal(as_bytes(pool).reshape(-1), expect.view(np.uint8).reshape(-1))
     assert read_and_clear_status(DEV) == 0
@@ -107,6 +111,15 @@ def test_commit_contract():
     bad[4] = 12 * 256 + 9
     before = pool.clone()
     copy_accepted_kv(pool, s, bad, 256)
+    torch.cuda.synchronize()
+    assert read_and_clear_status(DEV) == 2
+    assert torch.equal(pool.view(torch.int16), before.view(torch.int16)), "an invalid map must not write"
+    # The same on the check + move path (more slots than the one-launch commit takes).
+    pool, src, dst = small_commit_case(5, rows=3000, layers=2, pages=24)
+    bad = torch.as_tensor(dst, device=DEV).clone()
+    bad[2999] = -3
+    before = pool.clone()
+    copy_accepted_kv(pool, torch.as_tensor(src, device=DEV), bad, 256)
     torch.cuda.synchronize()
     assert read_and_clear_status(DEV) == 2
     assert torch.equal(pool.view(torch.int16), before.view(torch.int16)), "an invalid map must not write"
