@@ -9,7 +9,11 @@
 // so a KV tile staged in LDS is reused by every (node, query head) row of its group.
 // Long prefixes are cut into chunks (split-K) only as far as needed to give every
 // compute unit work; items are ordered longest first so the hardware dispatcher's
-// greedy assignment balances ragged contexts (an LPT schedule).
+// greedy assignment balances ragged contexts (an LPT schedule).  When that chunking
+// leaves a few rounds of items with the last round part-empty (more items than compute
+// units, at most kFillRounds rounds), the chunk target is lowered to the smallest
+// value whose item count still fits the same number of full rounds, so the rounds
+// fill with smaller, more even chunks.
 #include <stdint.h>
 
 #include <algorithm>
@@ -26,6 +30,7 @@ constexpr int kHeadDim = 128;
 constexpr int kMinChunkKeys = 64;   // shortest prefix chunk worth a partial result
 constexpr int kMaxChunkPages = 512; // page numbers a workgroup caches in LDS
 constexpr int kMaxTreeNodes = 1024; // tree slots a workgroup caches in LDS
+constexpr int64_t kFillRounds = 4;  // item rounds the chunk target is refitted for
 
 struct Item {
     int32_t r, h0, n0, kbeg, kend, flags, slot, hpw;
@@ -128,6 +133,40 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         return fail(TV_ERR_INVALID, "plan: chunk_keys %d exceeds %lld", chunk_keys, (long long)max_chunk);
     }
 
+    // Chunk length of a prefix of p keys (hpw heads per item) for chunk target `tau`:
+    // the longest multiple of 32 not above tau / hpw, then equalised over the chunks.
+    auto chunk_for = [&](int64_t p, int hpw, int64_t tau) -> int64_t {
+        int64_t chunk = std::min(round_up(std::max<int64_t>(kMinChunkKeys, tau / hpw), 32), max_chunk);
+        const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
+        chunk = round_up((p + nchunks - 1) / std::max<int64_t>(nchunks, 1), 32);
+        return chunk < 32 ? 32 : chunk;
+    };
+    auto items_for = [&](int64_t tau) -> int64_t {
+        int64_t n = 0;
+        for (int32_t r = 0; r < num_requests; ++r) {
+            const int64_t p = prefix_lens_host[r];
+            const int hpw = heads_per_group(node_counts_host[r], num_kv_heads);
+            const int npw = 64 / hpw;
+            const int64_t units = static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((node_counts_host[r] + npw - 1) / npw);
+            const int64_t chunk = chunk_for(p, hpw, tau);
+            n += units * (p > 0 ? (p + chunk - 1) / chunk : 1);
+        }
+        return n;
+    };
+    int64_t tau = target;
+    if (chunk_keys == 0) {
+        const int64_t now = items_for(target);
+        const int64_t rounds = (now + num_compute_units - 1) / num_compute_units;
+        if (now > num_compute_units && rounds <= kFillRounds) {
+            int64_t lo = 1, hi = target;   // items_for(hi) fits `rounds` full rounds
+            while (lo < hi) {
+                const int64_t mid = lo + (hi - lo) / 2;
+                if (items_for(mid) <= rounds * num_compute_units) hi = mid; else lo = mid + 1;
+            }
+            tau = lo;
+        }
+    }
+
     std::vector<Item> items;
     int32_t num_slots = 0, num_groups = 0;
     for (int32_t r = 0; r < num_requests; ++r) {
@@ -136,15 +175,7 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         const int npw = 64 / hpw;
         const int32_t groups = (num_kv_heads + hpw - 1) / hpw;
         const int32_t blocks = (t + npw - 1) / npw;
-        int64_t chunk;
-        if (chunk_keys > 0) {
-            chunk = chunk_keys;
-        } else {
-            chunk = std::min(round_up(std::max<int64_t>(kMinChunkKeys, target / hpw), 32), max_chunk);
-            const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
-            chunk = round_up((p + nchunks - 1) / std::max<int64_t>(nchunks, 1), 32);
-            if (chunk < 32) chunk = 32;
-        }
+        const int64_t chunk = chunk_keys > 0 ? chunk_keys : chunk_for(p, hpw, tau);
         const int32_t nchunks = p > 0 ? static_cast<int32_t>((p + chunk - 1) / chunk) : 1;
         for (int32_t hg = 0; hg < groups; ++hg) {
             for (int32_t nb = 0; nb < blocks; ++nb) {

@@ -32,6 +32,7 @@ constexpr int kMaxPlanRequests = 2048;
 constexpr int kMinChunkKeys = 64;
 constexpr int kMaxChunkPages = 512;
 constexpr int kXcds = 8;
+constexpr int64_t kFillRounds = 4;
 
 struct PlanArgs {
     const int32_t* prefix_lens;
@@ -67,6 +68,27 @@ __device__ int64_t block_scan(int64_t v, int64_t* scratch, int64_t* total) {
     if (t == kPlanThreads - 1) *total = inclusive;
     __syncthreads();
     return inclusive - v;
+}
+
+// Block-wide sum of one int64 per thread (kPlanThreads threads), returned to all.
+__device__ int64_t block_sum(int64_t v, int64_t* scratch) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int t = threadIdx.x;
+    __syncthreads();
+    if ((t & 63) == 0) scratch[t >> 6] = v;
+    __syncthreads();
+    int64_t total = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) total += scratch[w];
+    __syncthreads();   // every thread has read `scratch` before anyone reuses it
+    return total;
+}
+
+// The host planner's chunk length for a prefix of p keys and chunk target tau.
+__device__ __forceinline__ int64_t chunk_for(int64_t p, int hpw, int64_t tau, int64_t max_chunk) {
+    int64_t chunk = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), tau / hpw), 32), max_chunk);
+    const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
+    chunk = round_up((p + nchunks - 1) / max<int64_t>(nchunks, 1), 32);
+    return chunk < 32 ? 32 : chunk;
 }
 
 __global__ void __launch_bounds__(kPlanThreads)
@@ -106,6 +128,35 @@ plan_device_kernel(const PlanArgs a) {
     const int64_t target = max(static_cast<int64_t>(kMinChunkKeys), total_cost / a.compute_units);
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * B) / 32 * 32;
 
+    // 1b. The host's refit of the chunk target when the items leave the last of at most
+    // kFillRounds rounds part-empty: the same bisection, each probe a block sum.
+    auto items_for = [&](int64_t tau) -> int64_t {
+        int64_t n = 0;
+        for (int r = t; r < R; r += kPlanThreads) {
+            const int64_t p = max(0, a.prefix_lens[r]);
+            const int nodes = max(1, min(1024, a.node_counts[r]));
+            const int hpw = heads_per_group(nodes, a.num_kv_heads);
+            const int npw = 64 / hpw;
+            const int64_t units = static_cast<int64_t>((a.num_kv_heads + hpw - 1) / hpw) * ((nodes + npw - 1) / npw);
+            const int64_t chunk = chunk_for(p, hpw, tau, max_chunk);
+            n += units * (p > 0 ? (p + chunk - 1) / chunk : 1);
+        }
+        return block_sum(n, scan);
+    };
+    int64_t tau = target;
+    if (a.chunk_keys == 0) {
+        const int64_t now = items_for(target);
+        const int64_t rounds = (now + a.compute_units - 1) / a.compute_units;
+        if (now > a.compute_units && rounds <= kFillRounds) {
+            int64_t lo = 1, hi = target;
+            while (lo < hi) {
+                const int64_t mid = lo + (hi - lo) / 2;
+                if (items_for(mid) <= rounds * a.compute_units) hi = mid; else lo = mid + 1;
+            }
+            tau = lo;
+        }
+    }
+
     // 2. Chunking and per-request counts.  Requests are handled in contiguous runs per
     // thread so that one scan yields request-ordered offsets.
     const int per_thread = (R + kPlanThreads - 1) / kPlanThreads;
@@ -118,15 +169,7 @@ plan_device_kernel(const PlanArgs a) {
         const int npw = 64 / hpw;
         const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
         const int64_t NB = (n + npw - 1) / npw;
-        int64_t chunk;
-        if (a.chunk_keys > 0) {
-            chunk = a.chunk_keys;
-        } else {
-            chunk = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), target / hpw), 32), max_chunk);
-            const int64_t nc = p > 0 ? (p + chunk - 1) / chunk : 1;
-            chunk = round_up((p + nc - 1) / max<int64_t>(nc, 1), 32);
-            if (chunk < 32) chunk = 32;
-        }
+        const int64_t chunk = a.chunk_keys > 0 ? a.chunk_keys : chunk_for(p, hpw, tau, max_chunk);
         const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
         req_chunk[r] = static_cast<int32_t>(chunk);
         req_nchunks[r] = static_cast<int32_t>(nchunks);
@@ -336,7 +379,9 @@ extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, 
         return fail(TV_ERR_UNSUPPORTED, "plan_capacity: at most %d requests", kMaxPlanRequests);
     }
     // items <= CUs + sum_r G_r NB_r (1 + ceil(P_max / longest chunk)): a chunk is at least
-    // total/CUs keys per unit of cost unless it is capped by the LDS page cache.
+    // total/CUs keys per unit of cost unless it is capped by the LDS page cache.  The
+    // round-filling refit keeps the item count within the rounds that count needed, so
+    // it adds at most CUs - 1 items.
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
     const int64_t capped = (max_prefix + max_chunk - 1) / max_chunk;
     int64_t blocks = 0;
@@ -351,7 +396,7 @@ extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, 
     }
     // A forced chunk length gives every node-block group ceil(P / chunk) items.
     const int64_t items = chunk_keys > 0 ? blocks * std::max<int64_t>(1, (max_prefix + chunk_keys - 1) / chunk_keys)
-                                         : num_compute_units + blocks * (1 + capped);
+                                         : 2 * static_cast<int64_t>(num_compute_units) + blocks * (1 + capped);
     if (items > kMaxSortItems) {
         return fail(TV_ERR_UNSUPPORTED, "plan_capacity: %lld items exceed the device planner's %d",
                     static_cast<long long>(items), kMaxSortItems);

@@ -152,3 +152,32 @@ def test_plan_keeps_blocks_sharing_kv_on_one_xcd():
     lengths = [kend - kbeg for (_, _, _, kbeg, kend, _, _, _) in plain["items"].tolist()]
     assert lengths == sorted(lengths, reverse=True)
 
+
+
+def simulated_makespan(plan, counts, cus=256):
+    """Greedy list schedule of the plan's items in order onto `cus` CUs (8 XCDs, item i
+    on XCD i % 8), in 32-key tiles: the finish time of the last CU."""
+    import heapq
+    per_xcd = [[0] * (cus // 8) for _ in range(8)]
+    for index, (r, _, _, kbeg, kend, flags, _, hpw) in enumerate(plan["items"].tolist()):
+        tiles = (kend - kbeg + 31) // 32 + ((counts[r] + 31) // 32 if flags else 0)
+        heap = per_xcd[index % 8]
+        heapq.heapreplace(heap, heap[0] + hpw * tiles)
+    return max(max(h) for h in per_xcd)
+
+
+def test_plan_fills_its_rounds_of_work_items():
+    """A one-KV-head shard of the benchmark batch: the first chunking gives 288 items for
+    256 CUs, so the chunk target is refitted to fill two whole rounds (<= 512 items); the
+    last CU then finishes close to the average load instead of ~1.7x it."""
+    rng = np.random.default_rng(4)
+    prefixes = [int(x) for x in rng.integers(8192, 32769, size=64)]
+    plan = check_plan_covers(prefixes, [64] * 64, 1, 256)
+    assert 256 < plan["num_items"] <= 512
+    tiles = sum((p + 31) // 32 + 2 for p in prefixes)
+    assert simulated_makespan(plan, [64] * 64) < 1.1 * tiles / 256
+    # More than 4 rounds of items (or a forced chunk length) is left as first chunked.
+    rng = np.random.default_rng(5)
+    prefixes = [int(x) for x in rng.integers(0, 16385, size=16)] + [int(x) for x in rng.integers(2048, 8193, size=32)]
+    plan = make_plan(prefixes, [512] * 16 + [32] * 32, 8, 256, 256)
+    assert plan["num_items"] == 1152 and plan["num_groups"] == 0

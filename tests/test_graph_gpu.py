@@ -75,18 +75,30 @@ def batches():
     yield "long", ragged_metadata(2, [150000, 3], [64, 16])
 
 
+def shard_batches():
+    """(name, metadata, KV heads): one- and two-head shards, where the planner refits its
+    chunk target to fill whole rounds of work items."""
+    yield "cfg4/kv1", workloads.config4(DEV, kv_heads=1, requests=64).metadata, 1
+    yield "cfg5/kv2", workloads.config5(DEV, kv_heads=2).metadata, 2
+    rng = np.random.default_rng(8)
+    prefixes = [int(x) for x in rng.integers(0, 30000, size=34)]
+    counts = [int(x) for x in rng.choice([16, 32, 64], size=34)]
+    yield "ragged34", ragged_metadata(3, prefixes, counts, pool_pages=8192), 8
+
+
 @pytest.mark.parametrize("chunk_keys", [0, 64, 256])
 def test_device_plan_equals_host_plan(chunk_keys):
     cus = _device.compute_units(torch.cuda.current_device())
-    for name, meta in batches():
-        host = make_plan(meta.prefix_lengths, meta.node_counts_host, 8, meta.block_size, cus, chunk_keys)
+    cases = [(name, meta, 8) for name, meta in batches()] + (list(shard_batches()) if chunk_keys == 0 else [])
+    for name, meta, kv in cases:
+        host = make_plan(meta.prefix_lengths, meta.node_counts_host, kv, meta.block_size, cus, chunk_keys)
         print(f"[plan] {name} chunk={chunk_keys} items={host['num_items']} groups={host['num_groups']}", flush=True)
         if host["num_items"] > 8192:
             # Beyond the device planner's LDS sort: refused up front, never overrun.
             with pytest.raises(ValueError, match="exceed"):
-                device_plan(meta, chunk_keys=chunk_keys)
+                device_plan(meta, kv_heads=kv, chunk_keys=chunk_keys)
             continue
-        items, groups, counts, _ = device_plan(meta, chunk_keys=chunk_keys)
+        items, groups, counts, _ = device_plan(meta, kv_heads=kv, chunk_keys=chunk_keys)
         assert counts == [host["num_items"], host["num_groups"], host["num_partial_slots"], 0], name
         assert np.array_equal(items[:host["num_items"]], host["items"]), name
         assert np.array_equal(groups[:host["num_groups"]], host["groups"][:host["num_groups"]]), name
