@@ -221,14 +221,13 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
     if (blockIdx.x == 0 && blockIdx.y != 0) return;
     const int32_t n = static_cast<int32_t>(g.n);
     if (blockIdx.x == 0) {
-        // The dirty-row mover: slot lists in LDS, every row's test against all of them.
-        __shared__ int64_t s_src[kFusedMaxSlots], s_dst[kFusedMaxSlots];
+        // The dirty-row mover: every row's test against all slots, read from the (cached)
+        // slot lists; only a flag per row is kept in LDS, so the copy workgroups of this
+        // kernel are not limited by LDS occupancy.
         __shared__ uint8_t dirty[kFusedMaxSlots];
         int bad = 0;
         for (int32_t k = threadIdx.x; k < n; k += kMoveThreads) {
             const int64_t a = src[k], b = dst[k];
-            s_src[k] = a;
-            s_dst[k] = b;
             bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
         }
         if (__syncthreads_or(bad)) {
@@ -237,9 +236,9 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
         }
         int any = 0;
         for (int32_t i = threadIdx.x; i < n; i += kMoveThreads) {
-            const int64_t a = s_src[i], b = s_dst[i];
+            const int64_t a = src[i], b = dst[i];
             int d = 0;
-            for (int32_t k = 0; k < n; ++k) d |= (a == s_dst[k]) | (b == s_src[k]);
+            for (int32_t k = 0; k < n; ++k) d |= (a == dst[k]) | (b == src[k]);
             dirty[i] = static_cast<uint8_t>(d);
             any |= d;
         }
@@ -250,14 +249,14 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
             const int64_t row = u / upr, i = row % g.n, plane = row / g.n;
             if (!dirty[i]) continue;
             const char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
-            staging[u] = reinterpret_cast<const Unit*>(base + slot_offset(g, s_src[i]))[u % upr];
+            staging[u] = reinterpret_cast<const Unit*>(base + slot_offset(g, src[i]))[u % upr];
         }
         __syncthreads();
         for (int64_t u = threadIdx.x; u < rows * upr; u += kMoveThreads) {
             const int64_t row = u / upr, i = row % g.n, plane = row / g.n;
             if (!dirty[i]) continue;
             char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
-            reinterpret_cast<Unit*>(base + slot_offset(g, s_dst[i]))[u % upr] = staging[u];
+            reinterpret_cast<Unit*>(base + slot_offset(g, dst[i]))[u % upr] = staging[u];
         }
         return;
     }
