@@ -14,6 +14,8 @@
  *                         tree_gqa.py:32-111
  *   tv_copy_accepted_kv   accepted-only KV commit across both KV axes and all layers
  *                         replaces speculative/jetspec/state.py:64-86
+ *   tv_commit_slots       the batch's commit source/destination slots in one launch,
+ *                         replaces the per-request maps of state.py:746-798
  *   tv_rope_scatter       HF-order RoPE of the tree Q/K fused with the scratch
  *                         scatter of K/V, replaces speculative/jetspec/
  *                         tree_fusion.py:181-199 (rope_scatter_prevalidated)
@@ -115,6 +117,27 @@ int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6],
                         const int64_t* source_slots, const int64_t* destination_slots,
                         int64_t num_slots, void* workspace, int64_t workspace_bytes,
                         int64_t* payload_bytes_host, int32_t* status, void* stream);
+
+/*
+ * The commit maps of a whole batch in one launch, replacing the per-request host
+ * construction of speculative/jetspec/state.py:746-798 (`source =
+ * nodes.index_select(0, path)`, :780; `destination = _slots_for_blocks(owned +
+ * pending, len(path), B, start=cache_len)`, :782-785 with :54-61).  For request
+ * r < num_requests and i < len_r = path_offsets[r+1] - path_offsets[r]:
+ *     source_slots[path_offsets[r] + i]      = tree_slots[cu_seqlens[r] + paths[path_offsets[r] + i]]
+ *     pos = cache_lens[r] + i
+ *     destination_slots[path_offsets[r] + i] = block_tables[r*table_stride + pos/B]*B + pos%B
+ * (all int32 inputs; slots int64).  A path that is empty, does not start at node 0, repeats a
+ * node or names a node outside its tree (the reference's ValueErrors, :755-772), or a
+ * position past the row's table_width pages or a page outside [0, num_blocks), sets
+ * TV_STATUS_BAD_SLOT and writes -1 for every row of that request, so the following
+ * tv_copy_accepted_kv writes nothing.
+ */
+int tv_commit_slots(const int64_t* tree_slots, const int32_t* cu_seqlens, const int32_t* paths,
+                    const int32_t* path_offsets, const int32_t* block_tables, int64_t table_stride,
+                    int32_t table_width, const int32_t* cache_lens, int32_t num_requests,
+                    int32_t block_size, int64_t num_blocks, int64_t* source_slots,
+                    int64_t* destination_slots, int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* HF-order RoPE + tree K/V scatter  (speculative/jetspec/tree_fusion.py)     */

@@ -329,6 +329,60 @@ int64_t gcd64(int64_t a, int64_t b) {
 
 int64_t num_flag_words(int64_t n) { return (n + kCheckThreads - 1) / kCheckThreads; }
 
+// ------------------------------------------------------------------ commit slots
+// state.py:746-798 builds each request's commit maps on the host: the sources are its
+// accepted tree nodes' scratch slots (nodes.index_select(0, path), :780) and the
+// destinations the next len(path) canonical slots after cache_len through its owned +
+// pending pages (_slots_for_blocks, :54-61, :782-785), one host-to-device copy per
+// request.  Here one 64-lane wave per request builds both for the whole batch.  A path
+// that is empty, does not start at the root, repeats a node or names a node outside its tree, or
+// a destination beyond the request's table row or outside the pool, marks the request
+// bad: its rows get -1 (copy_accepted_kv then writes nothing) and a status bit is set.
+constexpr int kSlotWaves = 4;
+
+__global__ void __launch_bounds__(64 * kSlotWaves)
+commit_slots_kernel(const int64_t* __restrict__ tree_slots, const int32_t* __restrict__ cu,
+                    const int32_t* __restrict__ paths, const int32_t* __restrict__ path_off,
+                    const int32_t* __restrict__ tables, int64_t table_stride, int32_t table_width,
+                    const int32_t* __restrict__ cache_lens, int32_t num_requests, int32_t block_size,
+                    int64_t num_blocks, int64_t* __restrict__ src, int64_t* __restrict__ dst, int32_t* status) {
+    const int r = blockIdx.x * kSlotWaves + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= num_requests) return;
+    const int32_t begin = path_off[r], end = path_off[r + 1];
+    const int32_t q0 = cu[r], nodes = cu[r + 1] - q0;
+    const int64_t cache_len = cache_lens[r];
+    bool bad = begin >= end || nodes < 1 || cache_len < 0;
+    if (!bad && paths[begin] != 0) bad = true;
+    for (int32_t i = begin + lane; !bad && i < end; i += 64) {
+        const int32_t node = paths[i];
+        bool b = node < 0 || node >= nodes;
+        for (int32_t j = begin; j < i && !b; ++j) b = paths[j] == node;
+        const int64_t pos = cache_len + (i - begin);
+        const int64_t page_index = pos / block_size;
+        if (page_index >= table_width) {
+            b = true;
+        } else {
+            const int64_t page = tables[static_cast<int64_t>(r) * table_stride + page_index];
+            b = b || page < 0 || page >= num_blocks;
+        }
+        bad = bad || b;
+    }
+    bad = __any(bad);
+    if (bad && lane == 0) set_status(status, TV_STATUS_BAD_SLOT);
+    for (int32_t i = begin + lane; i < end; i += 64) {
+        if (bad) {
+            src[i] = -1;
+            dst[i] = -1;
+            continue;
+        }
+        const int64_t pos = cache_len + (i - begin);
+        const int64_t page = tables[static_cast<int64_t>(r) * table_stride + pos / block_size];
+        src[i] = tree_slots[q0 + paths[i]];
+        dst[i] = page * block_size + pos % block_size;
+    }
+}
+
 }  // namespace
 }  // namespace tv
 
@@ -484,4 +538,26 @@ extern "C" int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6], c
     if (rc != TV_OK) return rc;
     if (payload_bytes_host) *payload_bytes_host = payload;
     return TV_OK;
+}
+
+extern "C" int tv_commit_slots(const int64_t* tree_slots, const int32_t* cu_seqlens, const int32_t* paths,
+                               const int32_t* path_offsets, const int32_t* block_tables, int64_t table_stride,
+                               int32_t table_width, const int32_t* cache_lens, int32_t num_requests,
+                               int32_t block_size, int64_t num_blocks, int64_t* source_slots,
+                               int64_t* destination_slots, int32_t* status, void* stream) {
+    clear_error();
+    if (num_requests < 0 || block_size < 1 || num_blocks < 1 || table_width < 0 || table_stride < table_width) {
+        return fail(TV_ERR_INVALID, "commit_slots: invalid sizes");
+    }
+    if (num_requests == 0) return TV_OK;
+    if (!tree_slots || !cu_seqlens || !paths || !path_offsets || !cache_lens || !source_slots ||
+        !destination_slots || (table_width > 0 && !block_tables)) {
+        return fail(TV_ERR_INVALID, "commit_slots: null pointer");
+    }
+    const int64_t blocks = (static_cast<int64_t>(num_requests) + kSlotWaves - 1) / kSlotWaves;
+    hipLaunchKernelGGL(commit_slots_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(64 * kSlotWaves), 0,
+                       as_stream(stream), tree_slots, cu_seqlens, paths, path_offsets, block_tables, table_stride,
+                       table_width, cache_lens, num_requests, block_size, num_blocks, source_slots,
+                       destination_slots, status);
+    return check_launch("commit_slots");
 }

@@ -21,7 +21,7 @@ from .paged_backend import (
 )
 from .attention import store_kvcache
 from .tree_fusion import rope_scatter, rope_scatter_prevalidated
-from .state import copy_accepted_kv, _slots_for_blocks
+from .state import commit_slots, copy_accepted_kv, _slots_for_blocks
 from .serving_ops import accept_batch, accept_batch_device, accept_walk, build_child_maps, greedy_argmax
 from ._device import read_and_clear_status
 from ._lib import library
@@ -39,6 +39,7 @@ __all__ = [
     "rope_scatter",
     "rope_scatter_prevalidated",
     "copy_accepted_kv",
+    "commit_slots",
     "accept_batch",
     "accept_batch_device",
     "greedy_argmax",

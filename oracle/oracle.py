@@ -8,6 +8,7 @@ Contents (each restates the cited reference code):
   tree_attention_f64    paged_backend.py:116-213 (C, double precision)
   store_kvcache         layers/attention.py:15-45 (C, byte copy)
   copy_accepted_kv      speculative/jetspec/state.py:64-86 (C, gather then scatter)
+  commit_slots          speculative/jetspec/state.py:54-61 and :757-785 (numpy, per request)
   parent_chain          benchmarks/jetspec_numeric_oracles.py:24-58
   fp64_attention        benchmarks/jetspec_numeric_oracles.py:72-105
   mask_from_parents     benchmarks/jetspec_tree_kernel_qualification.py:102-107
@@ -155,6 +156,45 @@ def copy_accepted_kv(pool: np.ndarray, source, destination) -> int:
 
 
 # --------------------------------------------------------------------------- Python restatements
+def commit_slots(tree_slots, cu_seqlens, paths, path_offsets, block_tables, cache_lens, block_size: int,
+                 num_blocks: int):
+    """Commit source/destination slots of a batch, request by request (state.py:757-785).
+
+    A request whose path the reference would reject (empty, not rooted at node 0,
+    repeated or out-of-tree nodes, :770-773) or whose destinations leave its table row
+    or the pool gets -1 on all of its rows; returns (source, destination, bad) with
+    bad[r] True for such a request.
+    """
+    slots = np.asarray(tree_slots, dtype=np.int64)
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    path = np.asarray(paths, dtype=np.int64)
+    offsets = np.asarray(path_offsets, dtype=np.int64)
+    tables = np.asarray(block_tables, dtype=np.int64)
+    lens = np.asarray(cache_lens, dtype=np.int64)
+    source = np.full(path.size, -1, dtype=np.int64)
+    destination = np.full(path.size, -1, dtype=np.int64)
+    bad = np.zeros(lens.size, dtype=bool)
+    for r in range(lens.size):
+        indices = [int(x) for x in path[offsets[r]:offsets[r + 1]]]
+        nodes = int(cu[r + 1] - cu[r])
+        if (not indices or indices[0] != 0 or len(set(indices)) != len(indices) or min(indices) < 0
+                or max(indices) >= nodes or lens[r] < 0):
+            bad[r] = True
+            continue
+        positions = lens[r] + np.arange(len(indices))
+        pages = positions // block_size
+        if pages.max() >= tables.shape[1]:
+            bad[r] = True
+            continue
+        owned = tables[r, pages]
+        if owned.min() < 0 or owned.max() >= num_blocks:
+            bad[r] = True
+            continue
+        source[offsets[r]:offsets[r + 1]] = slots[cu[r] + np.asarray(indices)]
+        destination[offsets[r]:offsets[r + 1]] = owned * block_size + positions % block_size
+    return source, destination, bad
+
+
 def parent_chain(parents, chosen: int) -> list[int]:
     """Root-to-node indices by walking parents (jetspec_numeric_oracles.py:24-58)."""
     parents = [int(p) for p in parents]

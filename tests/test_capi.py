@@ -51,6 +51,13 @@ def test_entry_points_reject_bad_arguments_without_a_device():
     assert lib.tv_copy_accepted_kv(None, shape, stride, 2, None, None, 1, None, 0, None, None, None) \
         == _lib.TV_ERR_INVALID
     assert lib.tv_copy_accepted_kv_workspace_bytes(12, 36, 1024, 2) >= 2 * 36 * 12 * 1024 * 2
+    # commit_slots: bad sizes and null pointers fail on the host; no requests is a no-op.
+    assert lib.tv_commit_slots(None, None, None, None, None, 0, 0, None, 1, 0, 8, None, None, None, None) \
+        == _lib.TV_ERR_INVALID
+    assert lib.tv_commit_slots(None, None, None, None, None, 2, 4, None, 1, 16, 8, None, None, None, None) \
+        == _lib.TV_ERR_INVALID
+    assert lib.tv_commit_slots(None, None, None, None, None, 0, 0, None, 0, 16, 8, None, None, None, None) \
+        == _lib.TV_OK
     with pytest.raises(ValueError, match="block_size"):
         make_plan([10], [4], 8, 48, 256)
     with pytest.raises(ValueError, match="no tree nodes"):

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from jetspec_amd import copy_accepted_kv, read_and_clear_status, store_kvcache, workloads
+from jetspec_amd import commit_slots, copy_accepted_kv, read_and_clear_status, store_kvcache, workloads
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -149,3 +149,84 @@ def test_config3_commit_full_size_properties():
     untouched[dst] = False
     assert bool(torch.equal(before[:, untouched], after[:, untouched]))
     assert read_and_clear_status(DEV) == 0
+
+
+def commit_batch_case(seed, requests=24, block=16, width=6, pool_pages=256):
+    """A batch of accepted paths over shuffled page tables and scattered tree scratch slots."""
+    rng = np.random.default_rng(seed)
+    tables = rng.permutation(pool_pages)[:requests * width].reshape(requests, width).astype(np.int32)
+    counts = rng.integers(1, 40, size=requests)
+    cu = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    lens = rng.integers(0, (width - 2) * block, size=requests).astype(np.int32)
+    tree_slots = rng.permutation(pool_pages * block)[:cu[-1]].astype(np.int64)
+    paths, offsets = [], [0]
+    for r in range(requests):
+        depth = int(rng.integers(1, min(counts[r], block) + 1))
+        paths += [0] + rng.permutation(np.arange(1, counts[r]))[:depth - 1].tolist()
+        offsets.append(len(paths))
+    return tree_slots, cu, np.asarray(paths, np.int32), np.asarray(offsets, np.int32), tables, lens
+
+
+def run_commit_slots(case, block=16, pool_pages=256):
+    tree_slots, cu, paths, offsets, tables, lens = (torch.as_tensor(x, device=DEV) for x in case)
+    return commit_slots(tree_slots, cu, paths, offsets, tables, lens, block, pool_pages)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_commit_slots_match_oracle(seed):
+    requests = [1, 24, 300][seed]
+    pool_pages = max(256, requests * 6)
+    case = commit_batch_case(seed, requests=requests, pool_pages=pool_pages)
+    print(f"[commit_slots] seed={seed} requests={case[5].size} rows={case[2].size}", flush=True)
+    src, dst = run_commit_slots(case, pool_pages=pool_pages)
+    torch.cuda.synchronize()
+    esrc, edst, bad = oracle.commit_slots(*case, 16, pool_pages)
+    assert not bad.any()
+    assert np.array_equal(src.cpu().numpy(), esrc) and np.array_equal(dst.cpu().numpy(), edst)
+    assert read_and_clear_status(DEV) == 0
+
+
+def test_commit_slots_reject_like_the_reference():
+    tree_slots, cu, paths, offsets, tables, lens = commit_batch_case(4, requests=8)
+    paths, lens, tables = paths.copy(), lens.copy(), tables.copy()
+    rows = lambda r: slice(offsets[r], offsets[r + 1])
+    long_paths = [r for r in range(8) if offsets[r + 1] - offsets[r] >= 2]
+    a, b, c = long_paths[:3]
+    paths[rows(a)][0] = paths[rows(a)][1]          # not rooted at node 0
+    paths[offsets[b] + 1] = 0                      # repeated root
+    paths[offsets[c] + 1] = cu[c + 1] - cu[c]      # node outside the tree
+    lens[7] = 6 * 16 - 1 if offsets[8] - offsets[7] > 1 else lens[7]
+    tables[5, :] = 256                             # page outside the pool
+    case = (tree_slots, cu, paths, offsets, tables, lens)
+    print(f"[commit_slots] broken requests {a} {b} {c} 5 7", flush=True)
+    src, dst = run_commit_slots(case)
+    torch.cuda.synchronize()
+    esrc, edst, bad = oracle.commit_slots(*case, 16, 256)
+    assert bad[[a, b, c, 5]].all()
+    assert np.array_equal(src.cpu().numpy(), esrc) and np.array_equal(dst.cpu().numpy(), edst)
+    assert read_and_clear_status(DEV) == 2
+    with pytest.raises(ValueError, match="request count"):
+        commit_slots(*(torch.as_tensor(x, device=DEV) for x in case[:5]), torch.as_tensor(lens[:-1], device=DEV),
+                     16, 256)
+
+
+@pytest.mark.parametrize("broken", [False, True])
+def test_commit_slots_then_copy_matches_oracle_commit(broken):
+    case = list(commit_batch_case(9, requests=40))
+    if broken:
+        case[2] = case[2].copy()
+        case[2][case[3][3]] = 1                    # request 3's path no longer starts at the root
+    rng = np.random.default_rng(9)
+    pool = torch.as_tensor(rng.integers(-30000, 30000, size=(2, 3, 256, 16, 2, 64), dtype=np.int16),
+                           device=DEV).view(torch.bfloat16)
+    expect = pool.cpu().view(torch.int16).numpy().copy()
+    print(f"[commit_slots+copy] broken={broken}", flush=True)
+    src, dst = run_commit_slots(case)
+    copy_accepted_kv(pool, src, dst, 16)
+    torch.cuda.synchronize()
+    esrc, edst, bad = oracle.commit_slots(*case, 16, 256)
+    assert bad.any() == broken
+    if not broken:
+        oracle.copy_accepted_kv(expect, esrc, edst)
+    assert np.array_equal(pool.cpu().view(torch.int16).numpy(), expect)
+    assert read_and_clear_status(DEV) == (2 if broken else 0)

@@ -257,6 +257,56 @@ def test_copy_accepted_kv_oracle_is_gather_then_scatter():
     assert not np.array_equal(naive, got)
 
 
+def _enumerated_slots(pages, block_size):
+    """Canonical slots by walking the page list one page at a time (no div/mod)."""
+    return [page * block_size + offset for page in pages for offset in range(block_size)]
+
+
+def test_commit_slots_oracle_hand_kat():
+    # Pages [7, 3], 4-slot pages, 3 positions cached: the next three positions 3, 4, 5
+    # land at 7*4+3, then 3*4+0 and 3*4+1; node slots come from the tree's scratch slots.
+    src, dst, bad = oracle.commit_slots([90, 91, 92, 93], [0, 4], [0, 2, 3], [0, 3], [[7, 3]], [3], 4, 8)
+    assert dst.tolist() == [31, 12, 13] and src.tolist() == [90, 92, 93] and not bad.any()
+
+
+def test_commit_slots_oracle_matches_enumeration_and_rejects_reference_errors():
+    # state.py:770-773 rejects an empty path, a path not rooted at 0, repeated nodes and
+    # nodes outside the tree; the other requests of the batch are unaffected.
+    rng = np.random.default_rng(17)
+    block, requests = 16, 6
+    tables = rng.permutation(64)[:requests * 5].reshape(requests, 5)
+    lens = rng.integers(0, 50, size=requests)
+    counts = rng.integers(1, 12, size=requests)
+    cu = np.concatenate([[0], np.cumsum(counts)])
+    tree_slots = rng.permutation(4096)[:cu[-1]] + 2000
+    paths, offsets = [], [0]
+    for r in range(requests):
+        depth = int(rng.integers(1, counts[r] + 1))
+        paths += [0] + sorted(rng.permutation(np.arange(1, counts[r]))[:depth - 1].tolist())
+        offsets.append(len(paths))
+    src, dst, bad = oracle.commit_slots(tree_slots, cu, paths, offsets, tables, lens, block, 64)
+    assert not bad.any()
+    for r in range(requests):
+        rows = slice(offsets[r], offsets[r + 1])
+        n = offsets[r + 1] - offsets[r]
+        assert dst[rows].tolist() == _enumerated_slots(tables[r], block)[lens[r]:lens[r] + n]
+        assert src[rows].tolist() == [tree_slots[cu[r] + x] for x in paths[rows]]
+    for broken in ([1, 0], [0, 0], [0, counts[1]], [0, -1]):
+        p = list(paths[:offsets[1]]) + broken + list(paths[offsets[2]:])
+        o = [0, offsets[1], offsets[1] + len(broken)] + [x - (offsets[2] - offsets[1]) + len(broken)
+                                                          for x in offsets[3:]]
+        s2, d2, b2 = oracle.commit_slots(tree_slots, cu, p, o, tables, lens, block, 64)
+        assert b2.tolist() == [False, True] + [False] * (requests - 2)
+        assert (s2[o[1]:o[2]] == -1).all() and (d2[o[1]:o[2]] == -1).all()
+        assert np.array_equal(d2[:o[1]], dst[:offsets[1]]) and np.array_equal(d2[o[2]:], dst[offsets[2]:])
+    # past the table row, and a page outside the pool
+    _, _, b3 = oracle.commit_slots(tree_slots, cu, paths, offsets, tables, [5 * block - 1] + list(lens[1:]), block, 64)
+    assert b3[0] == (offsets[1] - offsets[0] > 1) and not b3[1:].any()
+    t4 = tables.copy(); t4[2, :] = 64
+    _, _, b4 = oracle.commit_slots(tree_slots, cu, paths, offsets, t4, lens, block, 64)
+    assert b4.tolist() == [r == 2 for r in range(requests)]
+
+
 # ----------------------------------------------------------------------------- acceptance / metrics
 def test_accept_walk_duplicate_sibling_kat():
     kat = KATS["accept_duplicate_siblings"]
