@@ -975,10 +975,12 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: Q/K/V rows must be 16-byte aligned");
     }
     // Tiles are addressed as page base + per-lane byte offset of up to 31 key rows, with
-    // 32-bit page and key-row byte strides.
+    // 32-bit page and key-row byte strides; the streaming loop also adds the step to the
+    // group's second KV head to that 32-bit lane offset.
     if (ks[0] < 0 || vs[0] < 0 || ks[1] < 0 || vs[1] < 0 || ks[2] < 0 || vs[2] < 0 ||
         ks[0] * 2 >= (int64_t{1} << 32) || vs[0] * 2 >= (int64_t{1} << 32) ||
-        ks[1] * 2 * kTileKeys >= (int64_t{1} << 31) || vs[1] * 2 * kTileKeys >= (int64_t{1} << 31)) {
+        ks[1] * 2 * kTileKeys >= (int64_t{1} << 31) || vs[1] * 2 * kTileKeys >= (int64_t{1} << 31) ||
+        ks[2] * 2 >= (int64_t{1} << 31) || vs[2] * 2 >= (int64_t{1} << 31)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: K/V strides out of range");
     }
     if (a->ancestor_words_per_row < 1 || a->ancestor_words_per_row > kMaxTreeSlots / 64) {
@@ -991,6 +993,11 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
     }
     if (a->num_requests < 1 || a->total_queries < 0 || a->num_items < 0 || a->num_groups < 0) {
         return fail(TV_ERR_INVALID, "tree_attention: invalid counts");
+    }
+    // Tree slots are cached as 32-bit values.
+    if (a->num_blocks < 0 || a->num_blocks * a->block_size >= (int64_t{1} << 31)) {
+        return fail(TV_ERR_UNSUPPORTED, "tree_attention: %lld pool pages of %d slots (at most 2^31 slots)",
+                    (long long)a->num_blocks, a->block_size);
     }
     if (a->num_items == 0) return TV_OK;
     if (!a->q || !a->k_pool || !a->v_pool || !a->out || !a->cu_seqlens_q || !a->prefix_lens || !a->node_counts ||

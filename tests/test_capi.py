@@ -64,6 +64,34 @@ def test_entry_points_reject_bad_arguments_without_a_device():
         make_plan([10], [0], 8, 256, 256)
 
 
+def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
+    """Checked before any launch: the kernel's per-lane tile offsets are 32-bit."""
+    lib = _lib.library()
+
+    def args(k_stride):
+        a = _lib.TreeAttentionArgs()
+        a.q = a.k_pool = a.v_pool = a.out = 0x10000
+        a.q_stride_row, a.q_stride_head = 8 * 128, 128
+        a.out_stride_row, a.out_stride_head = 8 * 128, 128
+        for i in range(4):
+            a.k_stride[i] = k_stride[i]
+            a.v_stride[i] = (256 * 2 * 128, 2 * 128, 128, 1)[i]
+        a.in_dtype = a.out_dtype = _lib.TV_BF16
+        a.num_q_heads, a.num_kv_heads, a.head_dim, a.block_size = 8, 2, 128, 256
+        a.scale = 128 ** -0.5
+        a.ancestor_words_per_row = 1
+        return a
+    for bad in ((1 << 31, 256, 128, 1),          # page stride of 4 GiB
+                (256 * 256, 1 << 25, 128, 1),   # 32 key rows span 2 GiB
+                (256 * 256, 256, 1 << 30, 1)):  # next KV head 2 GiB away
+        assert lib.tv_tree_attention(ctypes.byref(args(bad)), None) == _lib.TV_ERR_UNSUPPORTED, bad
+        assert b"strides out of range" in lib.tv_last_error()
+    big = args((256 * 256, 256, 128, 1))
+    big.num_blocks, big.num_requests = (1 << 31) // 256, 1
+    assert lib.tv_tree_attention(ctypes.byref(big), None) == _lib.TV_ERR_UNSUPPORTED
+    assert b"at most 2^31 slots" in lib.tv_last_error()
+
+
 def heads_per_group(nodes, kv_heads):
     h = 2 if nodes <= 32 else 1
     while h > 1 and h > kv_heads:
