@@ -221,14 +221,21 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
     if (blockIdx.x == 0 && blockIdx.y != 0) return;
     const int32_t n = static_cast<int32_t>(g.n);
     if (blockIdx.x == 0) {
-        // The dirty-row mover: every row's test against all slots, read from the (cached)
-        // slot lists; only a flag per row is kept in LDS, so the copy workgroups of this
-        // kernel are not limited by LDS occupancy.
+        // The dirty-row mover, the launch's longest workgroup: its all-pairs test
+        // decides when the kernel ends even when no row is dirty.  The slot lists go to
+        // LDS as 32-bit values (the host takes this path only for pools of fewer than
+        // 2^31 slots), padded to a multiple of 4 with -1, which equals no valid slot,
+        // and each row is tested against four slots of each list per 128-bit broadcast
+        // read.  18 KB of LDS per workgroup still lets a CU hold 8 of them.
+        __shared__ __attribute__((aligned(16))) int32_t s_src[kFusedMaxSlots], s_dst[kFusedMaxSlots];
         __shared__ uint8_t dirty[kFusedMaxSlots];
+        const int32_t n4 = (n + 3) & ~3;
         int bad = 0;
-        for (int32_t k = threadIdx.x; k < n; k += kMoveThreads) {
-            const int64_t a = src[k], b = dst[k];
-            bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
+        for (int32_t k = threadIdx.x; k < n4; k += kMoveThreads) {
+            const int64_t a = k < n ? src[k] : -1, b = k < n ? dst[k] : -1;
+            if (k < n) bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
+            s_src[k] = static_cast<int32_t>(a);
+            s_dst[k] = static_cast<int32_t>(b);
         }
         if (__syncthreads_or(bad)) {
             if (threadIdx.x == 0) set_status(status, TV_STATUS_BAD_SLOT);
@@ -236,9 +243,14 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
         }
         int any = 0;
         for (int32_t i = threadIdx.x; i < n; i += kMoveThreads) {
-            const int64_t a = src[i], b = dst[i];
+            const int32_t a = s_src[i], b = s_dst[i];
             int d = 0;
-            for (int32_t k = 0; k < n; ++k) d |= (a == dst[k]) | (b == src[k]);
+            for (int32_t k = 0; k < n4; k += 4) {
+                const int4 dk = *reinterpret_cast<const int4*>(&s_dst[k]);
+                const int4 sk = *reinterpret_cast<const int4*>(&s_src[k]);
+                d |= (a == dk.x) | (a == dk.y) | (a == dk.z) | (a == dk.w) | (b == sk.x) | (b == sk.y) |
+                     (b == sk.z) | (b == sk.w);
+            }
             dirty[i] = static_cast<uint8_t>(d);
             any |= d;
         }
@@ -506,7 +518,7 @@ extern "C" int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6], c
     void* staging = static_cast<char*>(workspace) + flag_bytes;
     hipStream_t s = as_stream(stream);
     int rc;
-    if (num_slots <= kFusedMaxSlots && 2 * layers <= 65535) {
+    if (num_slots <= kFusedMaxSlots && 2 * layers <= 65535 && pool_slots < (int64_t{1} << 31)) {
         const dim3 grid(static_cast<uint32_t>((num_slots + kMoveRows - 1) / kMoveRows + 1),
                         static_cast<uint32_t>(2 * layers));
         switch (unit) {
