@@ -24,6 +24,16 @@ store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
                      int64_t num_rows, int32_t units_per_row, int32_t* status) {
     const int64_t row_bytes = static_cast<int64_t>(units_per_row) * sizeof(Unit);
     for (int64_t row = blockIdx.x; row < num_rows; row += gridDim.x) {
+        const char* ksrc = key + row * key_stride_b;
+        const char* vsrc = value + row * value_stride_b;
+        // The row's first piece is loaded together with its slot (the key/value rows do
+        // not depend on it), so the slot lookup is not a round trip of its own.
+        const int32_t u0 = threadIdx.x;
+        Unit kv0{}, vv0{};
+        if (u0 < units_per_row) {
+            kv0 = reinterpret_cast<const Unit*>(ksrc)[u0];
+            vv0 = reinterpret_cast<const Unit*>(vsrc)[u0];
+        }
         const int64_t slot = slot_is_int64 ? static_cast<const int64_t*>(slots)[row]
                                            : static_cast<int64_t>(static_cast<const int32_t*>(slots)[row]);
         if (slot == -1) continue;
@@ -31,11 +41,13 @@ store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
             if (threadIdx.x == 0) set_status(status, TV_STATUS_BAD_SLOT);
             continue;
         }
-        const char* ksrc = key + row * key_stride_b;
-        const char* vsrc = value + row * value_stride_b;
         char* kdst = k_cache + slot * row_bytes;
         char* vdst = v_cache + slot * row_bytes;
-        for (int32_t u = threadIdx.x; u < units_per_row; u += blockDim.x) {
+        if (u0 < units_per_row) {
+            reinterpret_cast<Unit*>(kdst)[u0] = kv0;
+            reinterpret_cast<Unit*>(vdst)[u0] = vv0;
+        }
+        for (int32_t u = u0 + blockDim.x; u < units_per_row; u += blockDim.x) {
             const Unit kv = reinterpret_cast<const Unit*>(ksrc)[u];
             const Unit vv = reinterpret_cast<const Unit*>(vsrc)[u];
             reinterpret_cast<Unit*>(kdst)[u] = kv;
