@@ -7,7 +7,10 @@ Pages and scratch slots come from a shuffled pool whose unused rows are NaN, so 
 page, slot, mask bit or chunk boundary shows up either as NaN or as a gate failure
 (max-abs 2e-2, mean-abs 2e-3 against the oracle).  Together the cases cross the
 kernel's streaming and general loops, one- and two-head work items, page changes every
-1-16 tiles and chunk starts inside a page.
+1-16 tiles and chunk starts inside a page.  A second set draws larger batches (up to 48
+requests, prefixes up to 40k keys, trees up to 200 nodes) whose plans split prefixes and
+run several rounds of work items; there the oracle checks sampled rows of three requests
+per case.
 """
 from __future__ import annotations
 
@@ -79,4 +82,49 @@ def test_random_batch_matches_oracle(seed):
     assert torch.isfinite(out).all().item(), f"{label}: NaN padding was read"
     expect = oracle_rows(q, k, v, meta, 128 ** -0.5, list(range(meta.num_requests)))
     assert_within_gate(out, expect, label)
+    assert read_and_clear_status(q.device) == 0
+
+
+def large_case(seed):
+    rng = np.random.default_rng(seed)
+    requests = int(rng.integers(1, 49))
+    block = int(rng.choice([32, 64, 128, 256, 512]))
+    kv_heads = int(rng.choice([1, 2, 8], p=[0.3, 0.3, 0.4]))
+    prefixes = [int(x) for x in rng.integers(0, 40000, size=requests)]
+    counts = [int(rng.choice([1, 7, 16, 32, 33, 64, 100, 200])) for _ in range(requests)]
+    parents = [workloads.random_parents(n, int(rng.integers(1, 12)), rng) for n in counts]
+    prefix_pages = [-(-p // block) for p in prefixes]
+    scratch_pages = -(-sum(counts) // block) + 1
+    total = sum(prefix_pages) + scratch_pages + 2
+    order = rng.permutation(total)
+    tables, cursor = [], 0
+    for n in prefix_pages:
+        tables.append([int(x) for x in order[cursor:cursor + n]])
+        cursor += n
+    scratch = order[cursor:cursor + scratch_pages]
+    pool_slots = (scratch[:, None] * block + np.arange(block)).reshape(-1)[rng.permutation(scratch_pages * block)]
+    slots, off = [], 0
+    for n in counts:
+        slots.append(torch.as_tensor(pool_slots[off:off + n].astype(np.int64), device=DEV))
+        off += n
+    masks = [torch.as_tensor(workloads.ancestor_mask(p), device=DEV) for p in parents]
+    meta = PackedTreeMetadata.build(prefixes, tables, slots, masks, block)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    k = torch.randn((total, block, kv_heads, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    v = torch.randn((total, block, kv_heads, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    q = torch.randn((meta.total_queries, 4 * kv_heads, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    picks = sorted({int(x) for x in rng.choice(requests, size=min(3, requests), replace=False)})
+    label = (f"seed {seed}: R={requests} block={block} kv_heads={kv_heads} max prefix={max(prefixes)} "
+             f"max nodes={max(counts)} checked requests={picks}")
+    return q, k, v, meta, picks, label
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_large_random_batch_matches_oracle_on_sampled_rows(seed):
+    q, k, v, meta, picks, label = large_case(9100 + seed)
+    print(f"[random-large] {label}", flush=True)
+    out = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item(), label
+    assert_within_gate(out, oracle_rows(q, k, v, meta, 128 ** -0.5, picks, rows_per_request=8), label)
     assert read_and_clear_status(q.device) == 0
