@@ -46,46 +46,98 @@ int heads_per_group(int32_t nodes, int32_t kv_heads) {
 
 int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Cost of one key of a work item in quarter key-steps of a one-head item.  A two-head
+// item stages both heads' K/V but every wave still runs one head's 16 MFMAs per tile,
+// so a tile costs it ~1.25x a one-head tile, not 2x (per-workgroup timestamps: 1.30 vs
+// 1.03 us per tile on the mixed batch of config 5).  Weighting by the head count left
+// two-head chunks at half the length of one-head chunks of the same cost.
+int64_t cost_weight(int hpw) { return hpw == 2 ? 5 : 4; }
+
 // MI355X dispatches workgroup i of a launch to XCD i % 8, and each XCD has its own L2.
 // The node blocks of one (request, head group, prefix chunk) stream the same K/V, and
 // in longest-first order they sit next to each other, so they would land on different
-// XCDs and each XCD would pull that K/V from HBM.  Within every window of 64 items
-// (8 per XCD), the items of multi-block groups are taken first (keeping their order)
-// and the window is laid out column-major, item i -> position 8 * (i % 8) + i / 8:
-// 8 consecutive items share an XCD and are dispatched together.  Batches without
-// multi-block groups keep the plain longest-first order.
+// XCDs and each XCD would pull that K/V from HBM.  Items are therefore given ranks in
+// which such groups are whole blocks of 8, and every window of 64 ranks is laid out
+// column-major (rank i -> position 8 * (i % 8) + i / 8), so 8 consecutive ranks share an
+// XCD and are dispatched together; a partial last window keeps its ranks as positions.
+//   * When every group has a multiple of 8 items (trees of 512 or 1024 nodes among
+//     one-block trees), each group moves ahead of the at most 7 single items that
+//     precede it since the last multiple of 8: group items get rank (group items
+//     before) + 8 * floor(singles before / 8), and the j-th single moves behind every
+//     group so moved, which makes every group a run of whole 8-rank blocks.
+//   * Otherwise, within every window of 64 items the items of multi-block groups are
+//     taken first (keeping their order); a group that straddles two windows is split.
+// Batches without multi-block groups keep the plain longest-first order.
 constexpr int kXcds = 8;
 
 void place_for_xcds(std::vector<Item>& items) {
     constexpr size_t kWindow = kXcds * kXcds;
-    bool shared = false;
-    for (size_t i = 1; i < items.size() && !shared; ++i) {
-        const Item& a = items[i - 1];
-        const Item& b = items[i];
-        shared = a.r == b.r && a.hg == b.hg && a.chunk == b.chunk;
+    const size_t n = items.size();
+    auto same_stream = [&](size_t i, size_t j) {
+        return items[i].r == items[j].r && items[i].hg == items[j].hg && items[i].chunk == items[j].chunk;
+    };
+    bool shared = false, aligned = true;
+    for (size_t i = 0; i < n;) {
+        size_t j = i + 1;
+        while (j < n && same_stream(i, j)) ++j;
+        if (j - i > 1) {
+            shared = true;
+            aligned = aligned && (j - i) % kXcds == 0;
+        }
+        i = j;
     }
     if (!shared) return;
-    std::vector<Item> window;
-    for (size_t w = 0; w + kWindow <= items.size(); w += kWindow) {
-        window.assign(items.begin() + w, items.begin() + w + kWindow);
-        auto in_group = [&](size_t i) {
-            const Item& x = window[i];
-            auto same = [&](size_t j) {
-                return j < kWindow && window[j].r == x.r && window[j].hg == x.hg && window[j].chunk == x.chunk;
+    std::vector<Item> ranked(n);
+    if (aligned) {
+        std::vector<int64_t> singles_before(n + 1, 0);
+        std::vector<char> single(n);
+        for (size_t i = 0; i < n; ++i) {
+            single[i] = !((i > 0 && same_stream(i - 1, i)) || (i + 1 < n && same_stream(i, i + 1)));
+            singles_before[i + 1] = singles_before[i] + single[i];
+        }
+        auto floor8 = [](int64_t x) { return x / kXcds * kXcds; };
+        for (size_t i = 0; i < n; ++i) {
+            const int64_t sb = singles_before[i];
+            int64_t rank;
+            if (!single[i]) {
+                rank = (static_cast<int64_t>(i) - sb) + floor8(sb);
+            } else {
+                // p = first position whose rounded singles count exceeds this single's index;
+                // the group items before p are exactly the ones moved ahead of it.
+                size_t lo = i + 1, hi = n;
+                while (lo < hi) {
+                    const size_t mid = (lo + hi) / 2;
+                    if (floor8(singles_before[mid]) > sb) hi = mid; else lo = mid + 1;
+                }
+                rank = sb + (static_cast<int64_t>(lo) - singles_before[lo]);
+            }
+            ranked[static_cast<size_t>(rank)] = items[i];
+        }
+    } else {
+        ranked = items;
+        std::vector<Item> window;
+        for (size_t w = 0; w + kWindow <= n; w += kWindow) {
+            window.assign(items.begin() + w, items.begin() + w + kWindow);
+            auto in_group = [&](size_t i) {
+                const Item& x = window[i];
+                auto same = [&](size_t j) {
+                    return j < kWindow && window[j].r == x.r && window[j].hg == x.hg && window[j].chunk == x.chunk;
+                };
+                return same(i + 1) || (i > 0 && same(i - 1));
             };
-            return same(i + 1) || (i > 0 && same(i - 1));
-        };
-        std::vector<Item> order;
-        order.reserve(kWindow);
-        for (size_t i = 0; i < kWindow; ++i) {
-            if (in_group(i)) order.push_back(window[i]);
+            size_t k = w;
+            for (size_t i = 0; i < kWindow; ++i) {
+                if (in_group(i)) ranked[k++] = window[i];
+            }
+            for (size_t i = 0; i < kWindow; ++i) {
+                if (!in_group(i)) ranked[k++] = window[i];
+            }
         }
-        for (size_t i = 0; i < kWindow; ++i) {
-            if (!in_group(i)) order.push_back(window[i]);
-        }
-        for (size_t i = 0; i < kWindow; ++i) {
-            items[w + kXcds * (i % kXcds) + i / kXcds] = order[i];
-        }
+    }
+    const size_t full = n / kWindow * kWindow;
+    for (size_t i = 0; i < n; ++i) {
+        const size_t w = i - i % kWindow, k = i - w;
+        items[i < full ? w + kXcds * (k % kXcds) + k / kXcds : i] = ranked[i];
     }
 }
 
@@ -124,7 +176,7 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         const int npw = 64 / hpw;
         const int64_t groups = (num_kv_heads + hpw - 1) / hpw;
         const int64_t blocks = (t + npw - 1) / npw;
-        total_cost += groups * blocks * hpw * (static_cast<int64_t>(p) + t);
+        total_cost += groups * blocks * cost_weight(hpw) * (static_cast<int64_t>(p) + t);
     }
     const int64_t target = std::max<int64_t>(kMinChunkKeys, total_cost / num_compute_units);
     // Longest chunk whose pages fit the LDS page cache wherever it starts.
@@ -133,10 +185,11 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         return fail(TV_ERR_INVALID, "plan: chunk_keys %d exceeds %lld", chunk_keys, (long long)max_chunk);
     }
 
-    // Chunk length of a prefix of p keys (hpw heads per item) for chunk target `tau`:
-    // the longest multiple of 32 not above tau / hpw, then equalised over the chunks.
+    // Chunk length of a prefix of p keys (hpw heads per item) for chunk target `tau`
+    // (in cost units): the longest multiple of 32 keys whose cost is not above tau,
+    // then equalised over the chunks.
     auto chunk_for = [&](int64_t p, int hpw, int64_t tau) -> int64_t {
-        int64_t chunk = std::min(round_up(std::max<int64_t>(kMinChunkKeys, tau / hpw), 32), max_chunk);
+        int64_t chunk = std::min(round_up(std::max<int64_t>(kMinChunkKeys, tau / cost_weight(hpw)), 32), max_chunk);
         const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
         chunk = round_up((p + nchunks - 1) / std::max<int64_t>(nchunks, 1), 32);
         return chunk < 32 ? 32 : chunk;
@@ -192,7 +245,7 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
                     it.hpw = hpw;
                     // Node blocks of one (request, head group, chunk) share their K/V
                     // stream, so they get equal cost and stay adjacent after sorting.
-                    it.cost = static_cast<int64_t>(hpw) * ((it.kend - it.kbeg) + (it.flags ? t : 0));
+                    it.cost = cost_weight(hpw) * ((it.kend - it.kbeg) + (it.flags ? t : 0));
                     it.hg = hg;
                     it.chunk = c;
                     it.nb = nb;

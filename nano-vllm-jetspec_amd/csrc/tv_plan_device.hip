@@ -52,6 +52,11 @@ __device__ __forceinline__ int heads_per_group(int nodes, int kv_heads) {
 
 __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Cost of one key of a work item in quarter key-steps of a one-head item: a two-head
+// tile costs ~1.25x a one-head tile (each wave still runs one head's MFMAs).  The host
+// planner uses the same weights.
+__device__ __forceinline__ int64_t cost_weight(int hpw) { return hpw == 2 ? 5 : 4; }
+
 // Block-wide exclusive scan of one int per thread (kPlanThreads threads); returns the
 // thread's prefix and writes the total to *total.
 __device__ int64_t block_scan(int64_t v, int64_t* scratch, int64_t* total) {
@@ -85,7 +90,7 @@ __device__ int64_t block_sum(int64_t v, int64_t* scratch) {
 
 // The host planner's chunk length for a prefix of p keys and chunk target tau.
 __device__ __forceinline__ int64_t chunk_for(int64_t p, int hpw, int64_t tau, int64_t max_chunk) {
-    int64_t chunk = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), tau / hpw), 32), max_chunk);
+    int64_t chunk = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), tau / cost_weight(hpw)), 32), max_chunk);
     const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
     chunk = round_up((p + nchunks - 1) / max<int64_t>(nchunks, 1), 32);
     return chunk < 32 ? 32 : chunk;
@@ -117,7 +122,7 @@ plan_device_kernel(const PlanArgs a) {
         const int npw = 64 / hpw;
         const int64_t groups = (a.num_kv_heads + hpw - 1) / hpw;
         const int64_t blocks = (n + npw - 1) / npw;
-        my_cost += groups * blocks * hpw * (static_cast<int64_t>(p) + n);
+        my_cost += groups * blocks * cost_weight(hpw) * (static_cast<int64_t>(p) + n);
     }
     if (t == 0) shared_flag = 0;
     __syncthreads();
@@ -227,7 +232,7 @@ plan_device_kernel(const PlanArgs a) {
         for (int hg = 0; hg < G; ++hg) {
             for (int c = 0; c < nc; ++c) {
                 const int64_t kb = min(static_cast<int64_t>(p), c * chunk), ke = min(static_cast<int64_t>(p), (c + 1) * chunk);
-                const int64_t cost = static_cast<int64_t>(hpw) * ((ke - kb) + (c == nc - 1 ? n : 0));
+                const int64_t cost = cost_weight(hpw) * ((ke - kb) + (c == nc - 1 ? n : 0));
                 for (int nb = 0; nb < NB; ++nb) {
                     const int64_t idx = req_item_off[r] + (static_cast<int64_t>(hg) * nc + c) * NB + nb;
                     keys[idx] = (static_cast<uint64_t>(0x7fffffffu - static_cast<uint32_t>(cost)) << 32) |
@@ -304,33 +309,93 @@ plan_device_kernel(const PlanArgs a) {
     }
     if (t == 0) shared_flag = 0;
     __syncthreads();
+    // Bit 0: some stream has several items; bit 1: some stream's item count (its
+    // request's node blocks) is not a multiple of 8.
     for (int64_t i = 1 + t; i < num_items; i += kPlanThreads) {
         if (stream_id[i] == stream_id[i - 1]) atomicOr(&shared_flag, 1);
     }
+    for (int r = t; r < R; r += kPlanThreads) {
+        const int n = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        if (NB > 1 && NB % kXcds) atomicOr(&shared_flag, 2);
+    }
     __syncthreads();
-    const bool shared = shared_flag != 0;
+    const bool shared = (shared_flag & 1) != 0;
+    const bool aligned = (shared_flag & 2) == 0;
     constexpr int kWindow = kXcds * kXcds;
     const int64_t full = shared ? (num_items / kWindow) * kWindow : 0;
-    for (int64_t i = t; i < num_items; i += kPlanThreads) {
-        int64_t dest = i;
-        if (i < full) {
-            const int64_t w = i - i % kWindow;
-            const int k = static_cast<int>(i - w);
-            // Rank of item k in the window's "grouped first" order.
-            auto grouped = [&](int j) {
-                const int32_t s = stream_id[w + j];
-                return (j + 1 < kWindow && stream_id[w + j + 1] == s) || (j > 0 && stream_id[w + j - 1] == s);
-            };
-            const bool mine = grouped(k);
-            int rank = 0;
-            for (int j = 0; j < kWindow; ++j) {
-                if (j == k) continue;
-                const bool g = grouped(j);
-                if (mine ? (g && j < k) : (g || j < k)) ++rank;
-            }
-            dest = w + kXcds * (rank % kXcds) + rank / kXcds;
+    auto position_of = [&](int64_t rank) {
+        if (rank >= full) return rank;
+        const int64_t w = rank - rank % kWindow;
+        const int k = static_cast<int>(rank - w);
+        return w + kXcds * (k % kXcds) + k / kXcds;
+    };
+    if (shared && aligned) {
+        // Groups ahead of the at most 7 singles before them since the last multiple of
+        // 8: ranks from the number of single items before each sorted position.
+        constexpr int kPer = kMaxSortItems / kPlanThreads;
+        const int64_t i0 = static_cast<int64_t>(t) * kPer;
+        uint32_t single_bits = 0;
+        int64_t mine = 0;
+        for (int e = 0; e < kPer; ++e) {
+            const int64_t i = i0 + e;
+            if (i >= num_items) break;
+            const int32_t sid = stream_id[i];
+            const bool single = !((i > 0 && stream_id[i - 1] == sid) || (i + 1 < num_items && stream_id[i + 1] == sid));
+            single_bits |= static_cast<uint32_t>(single) << e;
+            mine += single;
         }
-        decode(i, a.items + dest * 8);
+        const int64_t before = block_scan(mine, scan, &totals[0]);   // syncs: stream_id reads are done
+        const int64_t singles_total = totals[0];
+        int64_t run = before;
+        for (int e = 0; e < kPer; ++e) {
+            const int64_t i = i0 + e;
+            if (i >= num_items) break;
+            stream_id[i] = static_cast<int32_t>(run);                 // now: singles before position i
+            run += (single_bits >> e) & 1u;
+        }
+        __syncthreads();
+        auto singles_before = [&](int64_t q) -> int64_t { return q < num_items ? stream_id[q] : singles_total; };
+        for (int e = 0; e < kPer; ++e) {
+            const int64_t i = i0 + e;
+            if (i >= num_items) break;
+            const int64_t sb = stream_id[i];
+            int64_t rank;
+            if (!((single_bits >> e) & 1u)) {
+                rank = (i - sb) + sb / kXcds * kXcds;
+            } else {
+                int64_t lo = i + 1, hi = num_items;   // first q with floor8(singles before q) > sb
+                while (lo < hi) {
+                    const int64_t mid = (lo + hi) >> 1;
+                    if (singles_before(mid) / kXcds * kXcds > sb) hi = mid; else lo = mid + 1;
+                }
+                rank = sb + (lo - singles_before(lo));
+            }
+            decode(i, a.items + position_of(rank) * 8);
+        }
+    } else {
+        for (int64_t i = t; i < num_items; i += kPlanThreads) {
+            int64_t rank = i;
+            if (i < full) {
+                const int64_t w = i - i % kWindow;
+                const int k = static_cast<int>(i - w);
+                // Rank of item k in the window's "grouped first" order.
+                auto grouped = [&](int j) {
+                    const int32_t s = stream_id[w + j];
+                    return (j + 1 < kWindow && stream_id[w + j + 1] == s) || (j > 0 && stream_id[w + j - 1] == s);
+                };
+                const bool mine = grouped(k);
+                int within = 0;
+                for (int j = 0; j < kWindow; ++j) {
+                    if (j == k) continue;
+                    const bool g = grouped(j);
+                    if (mine ? (g && j < k) : (g || j < k)) ++within;
+                }
+                rank = w + within;
+            }
+            decode(i, a.items + position_of(rank) * 8);
+        }
     }
     // Merge groups in (request, head group, block) order with their first partial slot.
     for (int r = r0; r < r1; ++r) {
