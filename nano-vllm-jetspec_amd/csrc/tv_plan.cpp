@@ -60,6 +60,9 @@ int64_t cost_weight(int hpw) { return hpw == 2 ? 5 : 4; }
 // which such groups are whole blocks of 8, and every window of 64 ranks is laid out
 // column-major (rank i -> position 8 * (i % 8) + i / 8), so 8 consecutive ranks share an
 // XCD and are dispatched together; a partial last window keeps its ranks as positions.
+// Odd windows mirror the columns (rank i -> XCD 7 - i / 8): the first column of a window
+// holds its longest items, and always giving it to XCD 0 overloaded XCD 0 by a few
+// percent over a launch.
 //   * When every group has a multiple of 8 items (trees of 512 or 1024 nodes among
 //     one-block trees), each group moves ahead of the at most 7 single items that
 //     precede it since the last multiple of 8: group items get rank (group items
@@ -137,7 +140,8 @@ void place_for_xcds(std::vector<Item>& items) {
     const size_t full = n / kWindow * kWindow;
     for (size_t i = 0; i < n; ++i) {
         const size_t w = i - i % kWindow, k = i - w;
-        items[i < full ? w + kXcds * (k % kXcds) + k / kXcds : i] = ranked[i];
+        const size_t column = (w / kWindow) % 2 ? kXcds - 1 - k / kXcds : k / kXcds;
+        items[i < full ? w + kXcds * (k % kXcds) + column : i] = ranked[i];
     }
 }
 

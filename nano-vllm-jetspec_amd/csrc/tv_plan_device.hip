@@ -329,7 +329,8 @@ plan_device_kernel(const PlanArgs a) {
         if (rank >= full) return rank;
         const int64_t w = rank - rank % kWindow;
         const int k = static_cast<int>(rank - w);
-        return w + kXcds * (k % kXcds) + k / kXcds;
+        const int column = (w / kWindow) % 2 ? kXcds - 1 - k / kXcds : k / kXcds;   // odd windows mirrored
+        return w + kXcds * (k % kXcds) + column;
     };
     if (shared && aligned) {
         // Groups ahead of the at most 7 singles before them since the last multiple of

@@ -146,8 +146,9 @@ def check_order(items, counts):
     """The dispatch order: longest first, up to the XCD placement of K/V-sharing groups.
 
     Items of one (request, head group, chunk) stream form a group.  Full 64-item
-    windows are column-major (position 8 * (k % 8) + k / 8 holds rank k), so ranks are
-    recovered by inverting that.  When every multi-item group has a multiple of 8 items,
+    windows are column-major (position 8 * (k % 8) + c holds rank k, with column
+    c = k / 8, mirrored to 7 - k / 8 in odd windows), so ranks are recovered by
+    inverting that.  When every multi-item group has a multiple of 8 items,
     each group must be whole aligned 8-rank blocks, and the rank order may differ from
     longest first only by groups moved ahead of at most 7 longer single items.  Otherwise
     every window must be at least as long as the next (placement only permutes within a
@@ -168,7 +169,8 @@ def check_order(items, counts):
     rank_of = list(range(n))
     for pos in range(full):
         w, k = pos - pos % XCD_WINDOW, pos % XCD_WINDOW
-        rank_of[pos] = w + 8 * (k % 8) + k // 8
+        column = 7 - k % 8 if (w // XCD_WINDOW) % 2 else k % 8
+        rank_of[pos] = w + 8 * column + k // 8
     by_rank = [None] * n
     for pos in range(n):
         by_rank[rank_of[pos]] = pos
