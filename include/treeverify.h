@@ -21,6 +21,8 @@
  *                         tree_fusion.py:181-199 (rope_scatter_prevalidated)
  *   tv_argmax_rows,       greedy acceptance: the target argmax and the tree walk,
  *   tv_tree_accept        replaces speculative/jetspec/serving_ops.py:55-90
+ *   tv_truncate_accepted  max_new_tokens / EOS cut of the accepted outputs and the
+ *                         packed commit paths, replaces batch_runtime.py:636-655
  *
  * Conventions
  *   - Every pointer argument is a device pointer unless its name ends in _host.
@@ -214,6 +216,30 @@ int tv_tree_accept(const int64_t* greedy, const void* token_ids, int32_t tokens_
                    const int32_t* cu_seqlens, int32_t num_requests, int32_t max_depth,
                    int32_t* paths, int32_t* lengths, int64_t* corrections,
                    int32_t* status, void* stream);
+
+/*
+ * The cut of each request's accepted outputs before its commit, replacing the host
+ * loop of speculative/jetspec/batch_runtime.py:636-655, on tv_tree_accept's outputs.
+ * For request r (path row r of path_stride int32, root-inclusive; lengths[r] draft
+ * tokens accepted; token_ids per packed node, int32 or int64):
+ *     values = token_ids[cu[r] + path[1..lengths[r]]] followed by corrections[r]
+ *     limit  = min(len(values), budgets[r])          (max_new_tokens - len(output_ids))
+ *     unless ignore_eos[r]: the first values[j], j < limit, equal to one of the
+ *     num_eos eos_token_ids sets limit = j + 1.
+ * Writes limits[r], emitted[r * path_stride + j] = values[j] for j < limit (-1 after),
+ * and the cut paths path[0..limit) back to back: commit_paths[commit_offsets[r] + j],
+ * commit_offsets[0..num_requests] (exclusive prefix sums of the limits), the packed
+ * paths tv_commit_slots takes; commit_paths needs room for num_requests * path_stride.
+ * A budget below 1, a length outside [0, path_stride) or a path node outside its
+ * tree sets TV_STATUS_BAD_REQUEST and gives that request limit 0 (no committed rows).
+ * One workgroup; num_requests == 0 writes nothing.
+ */
+int tv_truncate_accepted(const int32_t* paths, int32_t path_stride, const int32_t* lengths,
+                         const int64_t* corrections, const void* token_ids, int32_t tokens_is_int64,
+                         const int32_t* cu_seqlens, int32_t num_requests, const int32_t* budgets,
+                         const uint8_t* ignore_eos, const int64_t* eos_token_ids, int32_t num_eos,
+                         int32_t* limits, int64_t* emitted, int32_t* commit_paths,
+                         int32_t* commit_offsets, int32_t* status, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* packed tree attention  (speculative/jetspec/paged_backend.py:240-306)      */

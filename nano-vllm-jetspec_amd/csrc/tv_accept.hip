@@ -247,3 +247,111 @@ extern "C" int tv_tree_accept(const int64_t* greedy, const void* token_ids, int3
     hipLaunchKernelGGL(tree_accept_kernel, dim3(num_requests), dim3(64), 0, as_stream(stream), p);
     return check_launch("tree_accept");
 }
+
+// ------------------------------------------------------------ accepted-path truncation
+// batch_runtime.py:636-655 cuts each request's accepted outputs before it commits them:
+// values = tokens along the path after the root, then the correction; limit =
+// min(len(values), max_new_tokens - len(output_ids)); unless ignore_eos, the first EOS
+// among values[:limit] ends them (limit = its index + 1); the request emits
+// values[:limit] and caches path[:limit], which leaves its last emitted token uncached.
+// One workgroup walks the batch in chunks of kTruncThreads requests, one thread per
+// request, and a block scan of the limits lays the cut paths out back to back (the
+// packed form tv_commit_slots takes).
+namespace tv {
+namespace {
+constexpr int kTruncThreads = 1024;
+
+__global__ void __launch_bounds__(kTruncThreads)
+truncate_accepted_kernel(const int32_t* __restrict__ paths, int32_t stride, const int32_t* __restrict__ lengths,
+                         const int64_t* __restrict__ corrections, const void* __restrict__ tokens, int tokens64,
+                         const int32_t* __restrict__ cu, int32_t num_requests, const int32_t* __restrict__ budgets,
+                         const uint8_t* __restrict__ ignore_eos, const int64_t* __restrict__ eos, int32_t num_eos,
+                         int32_t* __restrict__ limits, int64_t* __restrict__ emitted,
+                         int32_t* __restrict__ commit_paths, int32_t* __restrict__ commit_offsets, int32_t* status) {
+    __shared__ int32_t scan[kTruncThreads];
+    __shared__ int32_t carry;
+    const int t = threadIdx.x;
+    if (t == 0) carry = 0;
+    __syncthreads();
+    for (int32_t base = 0; base < num_requests; base += kTruncThreads) {
+        const int32_t r = base + t;
+        int32_t limit = 0;
+        if (r < num_requests) {
+            const int32_t len = lengths[r];
+            const int32_t q0 = cu[r], nodes = cu[r + 1] - q0;
+            const int32_t* path = paths + static_cast<int64_t>(r) * stride;
+            bool ok = len >= 0 && len < stride && budgets[r] >= 1 && nodes >= 1;
+            for (int32_t j = 0; ok && j <= len; ++j) ok = path[j] >= 0 && path[j] < nodes;
+            auto value = [&](int32_t j) -> int64_t {
+                if (j == len) return corrections[r];
+                const int64_t row = q0 + path[j + 1];
+                return tokens64 ? static_cast<const int64_t*>(tokens)[row]
+                                : static_cast<int64_t>(static_cast<const int32_t*>(tokens)[row]);
+            };
+            if (!ok) {
+                set_status(status, TV_STATUS_BAD_REQUEST);
+            } else {
+                limit = min(len + 1, budgets[r]);
+                if (!ignore_eos[r]) {
+                    for (int32_t j = 0; j < limit; ++j) {
+                        const int64_t v = value(j);
+                        bool hit = false;
+                        for (int32_t e = 0; e < num_eos; ++e) hit = hit || v == eos[e];
+                        if (hit) {
+                            limit = j + 1;
+                            break;
+                        }
+                    }
+                }
+            }
+            limits[r] = limit;
+            for (int32_t j = 0; j < stride; ++j) emitted[static_cast<int64_t>(r) * stride + j] = j < limit ? value(j) : -1;
+        }
+        scan[t] = limit;
+        __syncthreads();
+        for (int off = 1; off < kTruncThreads; off <<= 1) {
+            const int32_t add = t >= off ? scan[t - off] : 0;
+            __syncthreads();
+            scan[t] += add;
+            __syncthreads();
+        }
+        const int32_t start = carry + scan[t] - limit;
+        if (r < num_requests) {
+            commit_offsets[r] = start;
+            const int32_t* path = paths + static_cast<int64_t>(r) * stride;
+            for (int32_t j = 0; j < limit; ++j) commit_paths[start + j] = path[j];
+        }
+        __syncthreads();
+        if (t == kTruncThreads - 1) carry += scan[t];
+        __syncthreads();
+    }
+    if (t == 0) commit_offsets[num_requests] = carry;
+}
+}  // namespace
+}  // namespace tv
+
+extern "C" int tv_truncate_accepted(const int32_t* paths, int32_t path_stride, const int32_t* lengths,
+                                    const int64_t* corrections, const void* token_ids, int32_t tokens_is_int64,
+                                    const int32_t* cu_seqlens, int32_t num_requests, const int32_t* budgets,
+                                    const uint8_t* ignore_eos, const int64_t* eos_token_ids, int32_t num_eos,
+                                    int32_t* limits, int64_t* emitted, int32_t* commit_paths,
+                                    int32_t* commit_offsets, int32_t* status, void* stream) {
+    using namespace tv;
+    clear_error();
+    if (num_requests < 0 || path_stride < 1 || num_eos < 0) {
+        return fail(TV_ERR_INVALID, "truncate_accepted: invalid request count, path stride or EOS count");
+    }
+    if (num_requests == 0) return TV_OK;
+    if (static_cast<int64_t>(num_requests) * path_stride > 0x7fffffff) {
+        return fail(TV_ERR_UNSUPPORTED, "truncate_accepted: too many path entries");
+    }
+    if (!paths || !lengths || !corrections || !token_ids || !cu_seqlens || !budgets || !ignore_eos || !limits ||
+        !emitted || !commit_paths || !commit_offsets || (num_eos > 0 && !eos_token_ids)) {
+        return fail(TV_ERR_INVALID, "truncate_accepted: null pointer");
+    }
+    hipLaunchKernelGGL(truncate_accepted_kernel, dim3(1), dim3(kTruncThreads), 0, as_stream(stream), paths,
+                       path_stride, lengths, corrections, token_ids, tokens_is_int64 != 0 ? 1 : 0, cu_seqlens,
+                       num_requests, budgets, ignore_eos, eos_token_ids, num_eos, limits, emitted, commit_paths,
+                       commit_offsets, status);
+    return check_launch("truncate_accepted");
+}

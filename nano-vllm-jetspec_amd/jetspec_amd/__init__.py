@@ -22,7 +22,8 @@ from .paged_backend import (
 from .attention import store_kvcache
 from .tree_fusion import rope_scatter, rope_scatter_prevalidated
 from .state import commit_slots, copy_accepted_kv, _slots_for_blocks
-from .serving_ops import accept_batch, accept_batch_device, accept_walk, build_child_maps, greedy_argmax
+from .serving_ops import (accept_batch, accept_batch_device, accept_walk, build_child_maps, greedy_argmax,
+                          truncate_accepted)
 from ._device import read_and_clear_status
 from ._lib import library
 
@@ -44,6 +45,7 @@ __all__ = [
     "accept_batch_device",
     "greedy_argmax",
     "accept_walk",
+    "truncate_accepted",
     "build_child_maps",
     "read_and_clear_status",
     "library",

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "tv_copy_accepted_kv_workspace_bytes",
     "tv_copy_accepted_kv",
     "tv_commit_slots",
+    "tv_truncate_accepted",
     "tv_tree_attention_plan",
     "tv_pack_ancestor_words",
     "tv_tree_attention",
@@ -147,6 +148,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_commit_slots.restype = c_int32
     lib.tv_commit_slots.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p,
                                     c_int32, c_int32, c_int64, c_void_p, c_void_p, c_void_p, c_void_p]
+    lib.tv_truncate_accepted.restype = c_int32
+    lib.tv_truncate_accepted.argtypes = [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_int32,
+                                         c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                         c_void_p, c_void_p, c_void_p]
     lib.tv_tree_attention_plan.restype = c_int32
     lib.tv_tree_attention_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32, c_int32,
                                            c_int32, c_int32, POINTER(c_int32), POINTER(c_int32),

@@ -14,6 +14,7 @@ Contents (each restates the cited reference code):
   mask_from_parents     benchmarks/jetspec_tree_kernel_qualification.py:102-107
   metadata_arrays       speculative/jetspec/packed_metadata.py:36-126 (host arrays)
   accept_walk           speculative/jetspec/serving_ops.py:55-90
+  truncate_accepted     speculative/jetspec/batch_runtime.py:636-655 (per request)
   argmax_flip_witness   benchmarks/jetspec_numeric_oracles.py:171-217
   rope_scatter_hf       speculative/jetspec/tree_fusion.py:20-82 and the eager HF RoPE
                         + scatter it replaces, models/qwen3.py:241-258 (numpy, exact
@@ -316,6 +317,25 @@ def accept_walk(greedy, tokens, depths, children, max_depth) -> dict:
     correction = greedy[path[-1]]
     return {"path": path, "accepted_length": len(path) - 1, "correction": correction,
             "outputs": [tokens[n] for n in path[1:]] + [correction]}
+
+
+def truncate_accepted(values, path, budget: int, ignore_eos: bool, eos_token_ids) -> dict:
+    """One request's max_new_tokens / EOS cut (batch_runtime.py:636-655).
+
+    values = the tokens along the accepted path after the root, then the correction;
+    budget = max_new_tokens - len(output_ids).  Returns limit, the emitted tokens
+    values[:limit] and the cached path path[:limit].
+    """
+    values, path = [int(x) for x in values], [int(x) for x in path]
+    if len(values) != len(path):
+        raise ValueError("one value per path node: the draft tokens after the root, then the correction")
+    limit = min(len(values), int(budget))
+    if not ignore_eos:
+        eos = {int(x) for x in eos_token_ids}
+        first = next((j for j, token in enumerate(values[:limit]) if token in eos), None)
+        if first is not None:
+            limit = first + 1
+    return {"limit": limit, "emitted": values[:limit], "path": path[:limit]}
 
 
 def argmax_flip_witness(actual: np.ndarray, reference: np.ndarray) -> dict:

@@ -18,7 +18,8 @@ import pytest
 import torch
 
 import oracle
-from jetspec_amd import accept_batch, accept_batch_device, greedy_argmax, workloads
+from jetspec_amd import (accept_batch, accept_batch_device, commit_slots, greedy_argmax, read_and_clear_status,
+                         truncate_accepted, workloads)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -149,3 +150,91 @@ def test_noncanonical_depth_raises():
     logits[0, tree.host_token_ids[child]] = 1.0     # the walk takes that child
     with pytest.raises(RuntimeError, match="canonical tail"):
         accept_batch(logits, trees, offsets, 15)
+
+
+def deep_accept_case(seed, sizes, max_depth=8, vocab=6):
+    """Random trees whose logits favour a child's token, run through the device walk."""
+    rng = np.random.default_rng(seed)
+    trees, offsets = random_batch(rng, sizes, vocab=vocab, max_depth=max_depth)
+    logits = torch.randn(offsets[-1], vocab, device=DEV)
+    for tree, lo in zip(trees, offsets):
+        for node, children in enumerate(tree.child_maps):
+            if children and rng.random() < 0.9:
+                logits[lo + node, int(rng.choice(list(children)))] += 6.0
+    tokens = torch.cat([t.token_ids for t in trees])
+    parents = torch.cat([t.parent_indices for t in trees])
+    depths = torch.cat([t.depth for t in trees])
+    cu = torch.tensor(offsets, dtype=torch.int32, device=DEV)
+    _, paths, lengths, corrections = accept_batch_device(logits, tokens, parents, depths, cu, max_depth)
+    return rng, trees, offsets, tokens, cu, paths, lengths, corrections
+
+
+def expected_cuts(trees, paths, lengths, corrections, budgets, ignore, eos):
+    cuts = []
+    for i, tree in enumerate(trees):
+        n = int(lengths[i])
+        path = [int(x) for x in paths[i, :n + 1]]
+        values = [tree.host_token_ids[x] for x in path[1:]] + [int(corrections[i])]
+        cuts.append(oracle.truncate_accepted(values, path, int(budgets[i]), bool(ignore[i]), eos))
+    return cuts
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_truncation_matches_oracle(seed):
+    sizes = [[1, 5, 16, 32, 64], [3] * 40, [16, 200, 1024, 64, 7, 33] * 5][seed]
+    rng, trees, offsets, tokens, cu, paths, lengths, corrections = deep_accept_case(100 + seed, sizes)
+    r = len(sizes)
+    budgets = torch.tensor(rng.integers(1, 12, size=r), dtype=torch.int32, device=DEV)
+    ignore = torch.tensor(rng.random(r) < 0.3, device=DEV)
+    eos = {int(x) for x in rng.choice(6, size=2, replace=False)}
+    print(f"[truncate] seed={seed} requests={r} eos={sorted(eos)}", flush=True)
+    limits, emitted, commit_paths, commit_offsets = truncate_accepted(paths, lengths, corrections, tokens, cu,
+                                                                      budgets, ignore, eos)
+    torch.cuda.synchronize()
+    host = [x.cpu() for x in (paths, lengths, corrections, budgets, ignore)]
+    cuts = expected_cuts(trees, *host[:3], host[3].tolist(), host[4].tolist(), eos)
+    assert limits.tolist() == [c["limit"] for c in cuts]
+    width = paths.shape[1]
+    assert emitted.tolist() == [c["emitted"] + [-1] * (width - c["limit"]) for c in cuts]
+    offsets_expected = np.concatenate([[0], np.cumsum([c["limit"] for c in cuts])]).tolist()
+    assert commit_offsets.tolist() == offsets_expected
+    assert commit_paths[:offsets_expected[-1]].tolist() == [x for c in cuts for x in c["path"]]
+    full = (host[1] + 1).tolist()
+    assert any(c["limit"] < f for c, f in zip(cuts, full)), "some request must be cut"
+    assert read_and_clear_status(DEV) == 0
+
+
+def test_truncation_bad_requests_and_commit_chain():
+    """Budget 0 gives limit 0 (status bit, no committed rows); the cut paths feed commit_slots."""
+    rng, trees, offsets, tokens, cu, paths, lengths, corrections = deep_accept_case(7, [16, 32, 5, 64])
+    budgets = torch.tensor([4, 0, 9, 2], dtype=torch.int32, device=DEV)
+    ignore = torch.tensor([False, False, True, False], device=DEV)
+    limits, emitted, commit_paths, commit_offsets = truncate_accepted(paths, lengths, corrections, tokens, cu,
+                                                                      budgets, ignore, [])
+    torch.cuda.synchronize()
+    assert limits[1].item() == 0 and (emitted[1] == -1).all().item()
+    assert read_and_clear_status(DEV) == 4
+    # Chain: the cut paths' commit maps equal the oracle's on the same cut paths.
+    n = int(commit_offsets[-1])
+    block, pool_pages = 16, 64
+    tables = torch.tensor(rng.permutation(pool_pages)[:4 * 4].reshape(4, 4), dtype=torch.int32, device=DEV)
+    cache_lens = torch.tensor([3, 17, 0, 40], dtype=torch.int32, device=DEV)
+    tree_slots = torch.tensor(rng.permutation(pool_pages * block)[:offsets[-1]], dtype=torch.int64, device=DEV)
+    live = [r for r in range(4) if limits[r].item() > 0]
+    keep = torch.tensor(live, device=DEV)
+    # Requests with limit 0 would be rejected (an empty path): commit the live ones only.
+    live_cu = torch.tensor(np.concatenate([[0], np.cumsum([offsets[r + 1] - offsets[r] for r in live])]),
+                           dtype=torch.int32, device=DEV)
+    live_slots = torch.cat([tree_slots[offsets[r]:offsets[r + 1]] for r in live])
+    live_paths = torch.cat([commit_paths[int(commit_offsets[r]):int(commit_offsets[r + 1])] for r in live])
+    live_offsets = torch.tensor(np.concatenate([[0], np.cumsum([int(limits[r]) for r in live])]), dtype=torch.int32,
+                                device=DEV)
+    src, dst = commit_slots(live_slots, live_cu, live_paths, live_offsets, tables[keep], cache_lens[keep], block,
+                            pool_pages)
+    torch.cuda.synchronize()
+    esrc, edst, bad = oracle.commit_slots(live_slots.cpu().numpy(), live_cu.cpu().numpy(), live_paths.cpu().numpy(),
+                                          live_offsets.cpu().numpy(), tables[keep].cpu().numpy(),
+                                          cache_lens[keep].cpu().numpy(), block, pool_pages)
+    assert not bad.any() and live_paths.numel() == n
+    assert src.tolist() == esrc.tolist() and dst.tolist() == edst.tolist()
+    assert read_and_clear_status(DEV) == 0

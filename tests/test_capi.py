@@ -58,6 +58,13 @@ def test_entry_points_reject_bad_arguments_without_a_device():
         == _lib.TV_ERR_INVALID
     assert lib.tv_commit_slots(None, None, None, None, None, 0, 0, None, 0, 16, 8, None, None, None, None) \
         == _lib.TV_OK
+    # truncate_accepted: bad counts and null pointers fail on the host; no requests is a no-op.
+    assert lib.tv_truncate_accepted(None, 0, None, None, None, 0, None, 1, None, None, None, 0, None, None, None,
+                                    None, None, None) == _lib.TV_ERR_INVALID
+    assert lib.tv_truncate_accepted(None, 9, None, None, None, 0, None, 1, None, None, None, 0, None, None, None,
+                                    None, None, None) == _lib.TV_ERR_INVALID
+    assert lib.tv_truncate_accepted(None, 9, None, None, None, 0, None, 0, None, None, None, 0, None, None, None,
+                                    None, None, None) == _lib.TV_OK
     with pytest.raises(ValueError, match="block_size"):
         make_plan([10], [4], 8, 48, 256)
     with pytest.raises(ValueError, match="no tree nodes"):

@@ -329,3 +329,23 @@ def test_argmax_flip_witness_kats():
     assert int(np.argmax(ties["reference"])) == ties["reference_argmax"]
     result = oracle.argmax_flip_witness([ties["actual"]], [ties["reference"]])
     assert result["argmax_flips"] == 1 and result["large_margin_violations"] == 0
+
+
+# ----------------------------------------------------------------------------- output truncation
+def test_truncate_oracle_reference_kats():
+    # tests/test_jetspec_batch_runtime.py:167-172: chain tree from token 9, every node
+    # accepted (the fixture's logits predict token + 1), EOS {11}: outputs [10, 11] and
+    # two cached rows (cache_len grows by 2, from prompt_length - 1 to prompt_length + 1).
+    cut = oracle.truncate_accepted([10, 11, 12], [0, 1, 2], 16, False, {11})
+    assert cut == {"limit": 2, "emitted": [10, 11], "path": [0, 1]}
+    # tests/test_jetspec_chunked_scheduler.py:310-316: the "ignore" request (max_new_tokens
+    # 4, ignore_eos) emits 5 at prefill, then [6, 7, 8] in one round: budget 3 keeps all.
+    assert oracle.truncate_accepted([6, 7, 8], [0, 1, 2], 3, True, {5})["emitted"] == [6, 7, 8]
+    # The budget cut without EOS, an EOS on the correction, and ignore_eos past an EOS.
+    assert oracle.truncate_accepted([6, 7, 8], [0, 1, 2], 2, False, {5}) == {"limit": 2, "emitted": [6, 7],
+                                                                             "path": [0, 1]}
+    assert oracle.truncate_accepted([1, 2, 63], [0, 4, 9], 16, False, {63})["limit"] == 3
+    assert oracle.truncate_accepted([63, 2], [0, 3], 16, True, {63})["limit"] == 2
+    assert oracle.truncate_accepted([63, 2], [0, 3], 16, False, {63})["limit"] == 1
+    with pytest.raises(ValueError):
+        oracle.truncate_accepted([1, 2], [0], 4, False, set())
