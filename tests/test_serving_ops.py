@@ -6,6 +6,7 @@ from pathlib import Path
 from types import SimpleNamespace
 
 import numpy as np
+import pytest
 import torch
 
 import oracle
@@ -52,3 +53,22 @@ def test_batch_walks_equal_oracle_walks_with_host_topology():
         expected = oracle.accept_walk(greedy[offsets[i]:offsets[i + 1]], tree.host_token_ids, tree.host_depths,
                                       tree.child_maps, 15)
         assert results[i] == expected
+
+
+def test_device_operators_reject_cpu_tensors():
+    """No operator has a CPU fallback: CPU inputs are refused before any library call
+    (the reference's test_cpu_is_not_a_graph_fallback, tests/test_jetspec_target_graph.py:31-33)."""
+    from jetspec_amd import commit_slots, truncate_accepted
+    from jetspec_amd.target_graph import GraphedTreeAttention, PackedVerifyGraph
+
+    with pytest.raises(ValueError, match="no CPU path"):
+        PackedVerifyGraph(torch.empty((2, 1, 1, 256, 8, 128)), torch.empty((16, 128)), 0.1, 4096)
+    with pytest.raises(ValueError, match="no CPU path"):
+        GraphedTreeAttention([16], 8, 256, max_prefix=512, device="cpu")
+    i32 = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="no CPU path"):
+        commit_slots(torch.zeros(1, dtype=torch.int64), i32, i32[:1], i32, torch.zeros((1, 1), dtype=torch.int32),
+                     i32[:1], 16, 4)
+    with pytest.raises(ValueError, match="no CPU path"):
+        truncate_accepted(torch.zeros((1, 2), dtype=torch.int32), i32[:1], torch.zeros(1, dtype=torch.int64),
+                          i32[:1], i32, i32[:1], torch.zeros(1, dtype=torch.bool), [2])
