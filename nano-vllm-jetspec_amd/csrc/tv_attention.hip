@@ -861,29 +861,55 @@ merge_partials_kernel(const AttnParams p) {
     const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
     if (r < 0 || r >= p.num_requests) return;
     const int wph = 8 / hpw;
-    const int tn = p.cnt[r], qbase = p.cu[r];
     const int wr = 8 * blockIdx.y + (threadIdx.x >> 5), quad = threadIdx.x & 31;
     const int wave = wr >> 5, c = wr & 31;
     const int hl = wave / wph;
     const int head = h0 + hl;
     const int node = n0 + 8 * (wave - hl * wph) + (c >> 2);
-    if (head >= p.num_kv_heads || node >= tn) return;
     const int qh = head * kGroups + (c & 3);
+    // Every partial of the group and the request's row offset are loaded together (a
+    // row past the tree or past the last head has slots too, never written; its loads
+    // stay in bounds and the row is dropped at the end), 8 partials at a time, with the
+    // running maximum rescaled between batches.  Up to 8 partials this is the plain
+    // maximum-then-sum.
     const float2* ml = p.ws_ml + static_cast<int64_t>(first) * kRowsPerItem + wr;
     const float* po = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * kHeadDim + 4 * quad;
-    float m = -INFINITY;
-#pragma unroll 4
-    for (int s = 0; s < ns; ++s) m = fmaxf(m, ml[static_cast<int64_t>(s) * kRowsPerItem].x);
-    const float mc = (m == -INFINITY ? 0.f : m) * p.c;
-    float l = 0.f;
+    const int tn = p.cnt[r], qbase = p.cu[r];
+    float m = -INFINITY, l = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int s = 0; s < ns; ++s) {
-        const float2 part = ml[static_cast<int64_t>(s) * kRowsPerItem];
-        const float w = __builtin_amdgcn_exp2f(part.x * p.c - mc);
-        l += part.y * w;
-        o += *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s) * kRowsPerItem * kHeadDim) * w;
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        float2 part[8];
+        f32x4 po4[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (s0 + k < ns) {
+                part[k] = ml[static_cast<int64_t>(s0 + k) * kRowsPerItem];
+                po4[k] = *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s0 + k) * kRowsPerItem * kHeadDim);
+            } else {
+                part[k] = make_float2(-INFINITY, 0.f);
+                po4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        float mb = m;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mb = fmaxf(mb, part[k].x);
+        const float mc = (mb == -INFINITY ? 0.f : mb) * p.c;
+        if (m != -INFINITY) {
+            const float keep = __builtin_amdgcn_exp2f(m * p.c - mc);
+            l *= keep;
+            o *= keep;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (s0 + k < ns) {
+                const float w = __builtin_amdgcn_exp2f(part[k].x * p.c - mc);
+                l += part[k].y * w;
+                o += po4[k] * w;
+            }
+        }
+        m = mb;
     }
+    if (head >= p.num_kv_heads || node >= tn) return;
     const float inv = 1.f / l;
     store_out4<T>(p, qbase + node, qh, 4 * quad, o * inv);
 }
