@@ -260,26 +260,20 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         return;
     }
 
-    // Page numbers of the prefix chunk and slots of the tree, validated, into LDS.
+    // Page numbers of the prefix chunk and slots of the tree, validated, into LDS, and
+    // this lane's Q rows into registers.  All of them are loaded before any is used
+    // (at most one page and two slots per thread), so the three lookups cost one round
+    // trip, not three.
+    static_assert(kMaxPages <= kThreads && kMaxTreeSlots <= 2 * kThreads, "one pass of page and slot loads");
     int32_t* pages = reinterpret_cast<int32_t*>(smem + kPagesOffset);
     int32_t* tslots = reinterpret_cast<int32_t*>(smem + kSlotsOffset);
-    for (int i = tid; i < npages; i += kThreads) {
-        int32_t pg = p.tables[static_cast<int64_t>(r) * p.t_s0 + page0 + i];
-        if (pg < 0 || pg >= p.num_blocks) {
-            set_status(p.status, TV_STATUS_BAD_PAGE);
-            pg = 0;
-        }
-        pages[i] = pg;
+    int32_t pg = 0;
+    int64_t sl[2] = {0, 0};
+    if (tid < npages) pg = p.tables[static_cast<int64_t>(r) * p.t_s0 + page0 + tid];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        if (tid + k * kThreads < tree_end) sl[k] = p.tree_slots[qbase + tid + k * kThreads];
     }
-    for (int i = tid; i < tree_end; i += kThreads) {
-        int64_t sl = p.tree_slots[qbase + i];
-        if (sl < 0 || sl >= pool_slots) {
-            set_status(p.status, TV_STATUS_BAD_PAGE);
-            sl = 0;
-        }
-        tslots[i] = static_cast<int32_t>(sl);
-    }
-
     // Q^T operand: lane (c, g) holds score row c, dims 16*st + 8*g + 0..7.
     V8 qb[8];
     {
@@ -290,6 +284,25 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             u32x4 raw = {0u, 0u, 0u, 0u};
             if (row_ok) raw = *reinterpret_cast<const u32x4*>(qrow + 16 * st);
             qb[st] = __builtin_bit_cast(V8, raw);
+        }
+    }
+    if (tid < npages) {
+        if (pg < 0 || pg >= p.num_blocks) {
+            set_status(p.status, TV_STATUS_BAD_PAGE);
+            pg = 0;
+        }
+        pages[tid] = pg;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = tid + k * kThreads;
+        if (i < tree_end) {
+            int64_t v = sl[k];
+            if (v < 0 || v >= pool_slots) {
+                set_status(p.status, TV_STATUS_BAD_PAGE);
+                v = 0;
+            }
+            tslots[i] = static_cast<int32_t>(v);
         }
     }
     // Retire the Q loads here: the tile loop then contains no compiler-tracked vector
