@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TV_ABI_VERSION 2
+#define TV_ABI_VERSION 3
 
 enum tv_error {
     TV_OK = 0,
@@ -293,6 +293,33 @@ int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* nod
                                   int32_t num_compute_units, int32_t chunk_keys, int32_t item_capacity,
                                   int32_t group_capacity, int32_t slot_capacity, int32_t* items,
                                   int32_t* groups, int32_t* counts, void* stream);
+
+/*
+ * Capacities like tv_tree_attention_plan_capacity, but holding for EVERY batch of one
+ * graph signature of speculative/jetspec/target_graph.py:24-27: num_requests requests,
+ * total_queries packed rows and (when > 0) sum_node_squares = sum_r T_r^2 (the
+ * qq_bias element count), whatever the individual node counts.  The reference's
+ * PackedTargetGraph replays one captured graph for all of them (target_graph.py:150-167),
+ * so a captured launch must be sized for the whole class:
+ *     max T <= min(1024, Q - (R - 1), floor(sqrt(sum T^2)))
+ *     node blocks <= Hkv * min((Q + 63 R) / 64, R * ceil(max T / 64)).
+ */
+int tv_tree_attention_plan_capacity_packed(int32_t total_queries, int32_t num_requests,
+                                           int64_t sum_node_squares, int32_t num_kv_heads,
+                                           int32_t block_size, int32_t num_compute_units,
+                                           int32_t chunk_keys, int64_t max_prefix,
+                                           tv_attention_plan_info* info);
+
+/*
+ * Whether `stream` is being captured into a graph: *capturing = 1 while capture is
+ * active, 0 when it is not, -1 when the capture was invalidated; *capture_id identifies
+ * the capture sequence (0 when not capturing).  The drop-in attention wrapper uses it
+ * to enqueue the live-metadata preparation (ancestor words + device plan) once at the
+ * start of each captured graph, so replays follow the metadata staged into the
+ * captured buffers (target_graph.py:55-75,150-167), as the reference's kernels do by
+ * reading prefix_lens in every program (paged_backend.py:138).
+ */
+int tv_stream_capture_info(void* stream, int32_t* capturing, uint64_t* capture_id);
 
 /*
  * Packs the request-local additive ancestor bias of PackedTreeMetadata

@@ -844,7 +844,11 @@ __global__ void __launch_bounds__(kThreads)
 tree_attention_kernel(const AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
     // A device-built plan launches a capacity grid; workgroups past its item count exit.
-    if (p.counts && static_cast<int>(blockIdx.x) >= p.counts[0]) return;
+    // A plan that overflowed its capacities has no items and reports it here.
+    if (p.counts) {
+        if (p.counts[3] != 0 && blockIdx.x == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+        if (static_cast<int>(blockIdx.x) >= p.counts[0]) return;
+    }
     const int32_t* d = p.items + 8 * blockIdx.x;
     const Item it{d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7]};
     if (it.r < 0 || it.r >= p.num_requests) {

@@ -17,6 +17,7 @@
 //      column-major), then the items and groups are written out.
 // Capacity overflow writes zero counts and an error flag instead of writing past the
 // caller's arrays.
+#include <math.h>
 #include <stdint.h>
 
 #include <algorithm>
@@ -433,34 +434,19 @@ plan_device_kernel(const PlanArgs a) {
 
 using namespace tv;
 
-extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, int32_t num_requests,
-                                               int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
-                                               int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info) {
-    clear_error();
-    if (!node_counts_host || !info || num_requests < 1 || num_kv_heads < 1 || block_size < 32 || block_size % 32 ||
-        num_compute_units < 1 || max_prefix < 0 || chunk_keys < 0 || chunk_keys % 32) {
-        return fail(TV_ERR_INVALID, "plan_capacity: invalid arguments");
-    }
-    if (num_requests > kMaxPlanRequests) {
-        return fail(TV_ERR_UNSUPPORTED, "plan_capacity: at most %d requests", kMaxPlanRequests);
-    }
-    // items <= CUs + sum_r G_r NB_r (1 + ceil(P_max / longest chunk)): a chunk is at least
-    // total/CUs keys per unit of cost unless it is capped by the LDS page cache.  The
-    // round-filling refit keeps the item count within the rounds that count needed, so
-    // it adds at most CUs - 1 items.
+namespace tv {
+namespace {
+
+// Capacities of a device-planned launch from the node-block total of the batch:
+// items <= 2 * CUs + blocks * (1 + ceil(P_max / longest chunk)).  A chunk is at least
+// total/CUs keys per unit of cost unless it is capped by the LDS page cache, and the
+// round-filling refit keeps the item count within the rounds that count needed, so it
+// adds at most CUs - 1 items.  A forced chunk length gives every node-block group
+// ceil(P_max / chunk) items.
+int fill_capacity(int64_t blocks, int32_t max_nodes, int32_t block_size, int32_t num_compute_units,
+                  int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info) {
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
     const int64_t capped = (max_prefix + max_chunk - 1) / max_chunk;
-    int64_t blocks = 0;
-    int32_t max_nodes = 1;
-    for (int32_t r = 0; r < num_requests; ++r) {
-        const int32_t n = node_counts_host[r];
-        if (n < 1 || n > 1024) return fail(TV_ERR_UNSUPPORTED, "plan_capacity: request %d has %d nodes", r, n);
-        max_nodes = n > max_nodes ? n : max_nodes;
-        const int hpw = n <= 32 && num_kv_heads >= 2 ? 2 : 1;
-        const int npw = 64 / hpw;
-        blocks += static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((n + npw - 1) / npw);
-    }
-    // A forced chunk length gives every node-block group ceil(P / chunk) items.
     const int64_t items = chunk_keys > 0 ? blocks * std::max<int64_t>(1, (max_prefix + chunk_keys - 1) / chunk_keys)
                                          : 2 * static_cast<int64_t>(num_compute_units) + blocks * (1 + capped);
     if (items > kMaxSortItems) {
@@ -472,6 +458,86 @@ extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, 
     info->num_partial_slots = static_cast<int32_t>(items);
     info->ancestor_words_per_row = (max_nodes + 63) / 64;
     info->workspace_bytes = (items * 256 * 128 * 4 + 255) / 256 * 256 + (items * 256 * 8 + 255) / 256 * 256;
+    return TV_OK;
+}
+
+bool capacity_args_ok(int32_t num_requests, int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
+                      int32_t chunk_keys, int64_t max_prefix) {
+    return num_requests >= 1 && num_kv_heads >= 1 && block_size >= 32 && block_size % 32 == 0 &&
+           num_compute_units >= 1 && max_prefix >= 0 && chunk_keys >= 0 && chunk_keys % 32 == 0;
+}
+
+}  // namespace
+}  // namespace tv
+
+extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, int32_t num_requests,
+                                               int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
+                                               int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info) {
+    clear_error();
+    if (!node_counts_host || !info ||
+        !capacity_args_ok(num_requests, num_kv_heads, block_size, num_compute_units, chunk_keys, max_prefix)) {
+        return fail(TV_ERR_INVALID, "plan_capacity: invalid arguments");
+    }
+    if (num_requests > kMaxPlanRequests) {
+        return fail(TV_ERR_UNSUPPORTED, "plan_capacity: at most %d requests", kMaxPlanRequests);
+    }
+    int64_t blocks = 0;
+    int32_t max_nodes = 1;
+    for (int32_t r = 0; r < num_requests; ++r) {
+        const int32_t n = node_counts_host[r];
+        if (n < 1 || n > 1024) return fail(TV_ERR_UNSUPPORTED, "plan_capacity: request %d has %d nodes", r, n);
+        max_nodes = n > max_nodes ? n : max_nodes;
+        const int hpw = n <= 32 && num_kv_heads >= 2 ? 2 : 1;
+        const int npw = 64 / hpw;
+        blocks += static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((n + npw - 1) / npw);
+    }
+    return fill_capacity(blocks, max_nodes, block_size, num_compute_units, chunk_keys, max_prefix, info);
+}
+
+extern "C" int tv_tree_attention_plan_capacity_packed(int32_t total_queries, int32_t num_requests,
+                                                      int64_t sum_node_squares, int32_t num_kv_heads,
+                                                      int32_t block_size, int32_t num_compute_units,
+                                                      int32_t chunk_keys, int64_t max_prefix,
+                                                      tv_attention_plan_info* info) {
+    clear_error();
+    if (!info || total_queries < num_requests ||
+        !capacity_args_ok(num_requests, num_kv_heads, block_size, num_compute_units, chunk_keys, max_prefix)) {
+        return fail(TV_ERR_INVALID, "plan_capacity_packed: invalid arguments");
+    }
+    if (num_requests > kMaxPlanRequests) {
+        return fail(TV_ERR_UNSUPPORTED, "plan_capacity_packed: at most %d requests", kMaxPlanRequests);
+    }
+    // Largest node count: every other request has at least one node, and when the sum of
+    // squares is given, max_r T_r^2 <= sum_r T_r^2.
+    int64_t max_nodes = static_cast<int64_t>(total_queries) - (num_requests - 1);
+    if (sum_node_squares > 0) {
+        int64_t root = static_cast<int64_t>(sqrt(static_cast<double>(sum_node_squares)));
+        while (root * root > sum_node_squares) --root;
+        while ((root + 1) * (root + 1) <= sum_node_squares) ++root;
+        max_nodes = std::min(max_nodes, root);
+    }
+    max_nodes = std::min<int64_t>(max_nodes, 1024);
+    // A request of T nodes has at most num_kv_heads * ceil(T / 64) node blocks (two-head
+    // groups of trees of <= 32 nodes have fewer), and sum_r ceil(T_r / 64) is at most
+    // (Q + 63 R) / 64 and at most R * ceil(max T / 64).
+    const int64_t per_head = std::min<int64_t>((static_cast<int64_t>(total_queries) + 63 * num_requests) / 64,
+                                               static_cast<int64_t>(num_requests) * ((max_nodes + 63) / 64));
+    const int64_t blocks = static_cast<int64_t>(num_kv_heads) * per_head;
+    return fill_capacity(blocks, static_cast<int32_t>(max_nodes), block_size, num_compute_units, chunk_keys,
+                         max_prefix, info);
+}
+
+extern "C" int tv_stream_capture_info(void* stream, int32_t* capturing, uint64_t* capture_id) {
+    clear_error();
+    if (!capturing || !capture_id) return fail(TV_ERR_INVALID, "stream_capture_info: null output");
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    const hipError_t err = hipStreamGetCaptureInfo(as_stream(stream), &status, &id);
+    if (err != hipSuccess) {
+        return fail(TV_ERR_LAUNCH, "stream_capture_info: %s", hipGetErrorString(err));
+    }
+    *capturing = status == hipStreamCaptureStatusActive ? 1 : (status == hipStreamCaptureStatusNone ? 0 : -1);
+    *capture_id = status == hipStreamCaptureStatusNone ? 0 : static_cast<uint64_t>(id);
     return TV_OK;
 }
 

@@ -7,12 +7,12 @@ device entry point raises ``RuntimeError`` naming the problem.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_uint64, c_void_p
 from pathlib import Path
 import threading
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libtreeverify.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TV_OK = 0
 TV_ERR_INVALID = -1
@@ -51,6 +51,8 @@ EXPORTED_SYMBOLS = (
     "tv_bias_from_ancestor_words",
     "tv_tree_attention_plan_capacity",
     "tv_tree_attention_plan_device",
+    "tv_tree_attention_plan_capacity_packed",
+    "tv_stream_capture_info",
 )
 
 
@@ -179,6 +181,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_tree_attention_plan_device.restype = c_int32
     lib.tv_tree_attention_plan_device.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                                   c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]
+    lib.tv_tree_attention_plan_capacity_packed.restype = c_int32
+    lib.tv_tree_attention_plan_capacity_packed.argtypes = [c_int32, c_int32, c_int64, c_int32, c_int32, c_int32,
+                                                           c_int32, c_int64, POINTER(PlanInfo)]
+    lib.tv_stream_capture_info.restype = c_int32
+    lib.tv_stream_capture_info.argtypes = [c_void_p, POINTER(c_int32), POINTER(c_uint64)]
     lib.tv_tree_accept.restype = c_int32
     lib.tv_tree_accept.argtypes = [c_void_p, c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_int32, c_void_p,
                                    c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]

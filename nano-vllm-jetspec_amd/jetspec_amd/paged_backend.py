@@ -8,11 +8,30 @@ bf16/f16 MFMA products, fp32 accumulation and online softmax, and probabilities
 rounded to the operand type for the P.V product (as the reference's gqa backend,
 tree_gqa.py:102-105).
 
-Per metadata object the wrapper derives, once, on the launch stream:
-  * the work plan (tv_tree_attention_plan over the host prefix/node counts),
-  * the ancestor bit rows (tv_pack_ancestor_words over qq_bias),
-so the 36 per-layer launches of one verify round reuse them.  A launch allocates
-only its output and (when the plan splits prefixes) a partial-result workspace.
+Two launch modes, chosen per call:
+
+* Eager (the stream is not capturing).  Per metadata object the wrapper derives,
+  once: the work plan (tv_tree_attention_plan over the host prefix/node counts) and
+  the ancestor bit rows (tv_pack_ancestor_words over qq_bias, or the words the
+  serving constructor built on the device).  Per (metadata, K/V pool, stream) it
+  keeps a filled argument block and, when the plan splits prefixes, one partial-
+  result workspace that the 36 per-layer launches of a round reuse in stream order.
+  A steady-state call allocates only its output.  Metadata objects are treated as
+  immutable here, as the reference's frozen dataclass is: an object whose device
+  tensors are rewritten in place must be replayed through a captured graph.
+* Captured (torch.cuda.is_current_stream_capturing()).  The reference's
+  PackedTargetGraph (target_graph.py:55-167) captures the forward once against a
+  staged metadata object and replays it after copy_-ing each round's metadata into
+  that object; its kernels read prefix lengths and node counts from device memory
+  (paged_backend.py:138).  So under capture this wrapper plans on the device too:
+  the first call of a capture on a metadata object enqueues the ancestor words
+  (from the live qq_bias) and the device planner (from the live prefix_lens and
+  node_counts), sized for every batch of the graph signature (request count,
+  packed rows, qq_bias elements); each call then launches the attention and merge
+  kernels on capacity grids that read the live counts.  Replays therefore follow
+  the staged metadata.  The capture-mode buffers belong to the metadata object,
+  which must outlive the graphs that captured it (PackedTargetGraph keeps it in the
+  graph entry), and graphs sharing one metadata object must not replay concurrently.
 """
 from __future__ import annotations
 
@@ -31,7 +50,8 @@ _derived_lock = threading.Lock()
 
 
 def _validate(q, k_pool, v_pool, metadata, groups, output_dtype) -> torch.dtype:
-    """Geometry/device/dtype checks of tree_attention.py:21-37; returns the output dtype."""
+    """Geometry/device/dtype checks of tree_attention.py:21-37, then the kernel's own
+    limits; returns the output dtype."""
     if q.ndim != 3 or q.shape[0] != metadata.total_queries:
         raise ValueError("packed queries do not match the metadata")
     if k_pool.ndim != 4 or k_pool.shape != v_pool.shape or k_pool.shape[1] != metadata.block_size:
@@ -87,16 +107,24 @@ def _release(key: int) -> None:
         _derived.pop(key, None)
 
 
-def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
-    """Work plan and ancestor bits of `metadata` for `num_kv_heads`, built once per object."""
+def _per_metadata(metadata) -> dict:
+    """The derived-state dictionary of one metadata object (dropped with the object)."""
     key = id(metadata)
+    per_meta = _derived.get(key)
+    if per_meta is not None:
+        return per_meta
+    _check_metadata_buffers(metadata)
     with _derived_lock:
         per_meta = _derived.get(key)
-    if per_meta is None:
-        _check_metadata_buffers(metadata)
-        with _derived_lock:
-            per_meta = _derived.setdefault(key, {})
-        weakref.finalize(metadata, _release, key)
+        if per_meta is None:
+            per_meta = _derived[key] = {}
+            weakref.finalize(metadata, _release, key)
+    return per_meta
+
+
+def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
+    """Work plan and ancestor bits of `metadata` for `num_kv_heads`, built once per object."""
+    per_meta = _per_metadata(metadata)
     lib = _lib.library()
     device = metadata.tree_slots.device
     words = per_meta.get("ancestor_words")
@@ -150,43 +178,46 @@ def make_plan(prefix_lengths, node_counts, num_kv_heads: int, block_size: int, c
             "num_partial_slots": info.num_partial_slots, "workspace_bytes": int(info.workspace_bytes)}
 
 
-def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> torch.Tensor:
-    lib = _lib.library()
-    device = q.device
-    num_kv_heads = int(k_pool.shape[2])
-    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
-        q = q.contiguous()
-    state = derived_state(metadata, num_kv_heads, chunk_keys=chunk_keys)
-    workspace = None
-    if state["workspace_bytes"]:
-        workspace = torch.empty(state["workspace_bytes"], dtype=torch.uint8, device=device)
-    a = _lib.TreeAttentionArgs()
-    a.q = q.data_ptr()
-    a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
+def fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads: int, status) -> None:
+    """The metadata, K/V pool and geometry fields of a tv_tree_attention_args block."""
     a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
     for i in range(4):
         a.k_stride[i] = k_pool.stride(i)
         a.v_stride[i] = v_pool.stride(i)
     a.num_blocks = int(k_pool.shape[0])
-    a.in_dtype = _device.dtype_code(q.dtype)
-    a.out = out.data_ptr()
-    a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
-    a.out_dtype = _device.dtype_code(out.dtype)
+    a.in_dtype = _device.dtype_code(k_pool.dtype)
     a.cu_seqlens_q = metadata.cu_seqlens_q.data_ptr()
     a.prefix_lens = metadata.prefix_lens.data_ptr()
     a.node_counts = metadata.node_counts.data_ptr()
     a.block_tables = metadata.block_tables.data_ptr()
     a.block_table_stride = metadata.block_tables.stride(0)
     a.tree_slots = metadata.tree_slots.data_ptr()
-    a.ancestor_words = state["ancestor_words"].data_ptr()
-    a.ancestor_words_per_row = state["words_per_row"]
     a.num_requests = metadata.num_requests
     a.total_queries = metadata.total_queries
-    a.num_q_heads = int(q.shape[1])
+    a.num_q_heads = 4 * num_kv_heads
     a.num_kv_heads = num_kv_heads
-    a.head_dim = int(q.shape[2])
+    a.head_dim = int(k_pool.shape[3])
     a.block_size = metadata.block_size
-    a.scale = float(scale)
+    a.status = status.data_ptr()
+
+
+def _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads: int, chunk_keys: int, stream: int):
+    """Filled argument block of one (metadata, K/V pool, stream): everything but Q, O and scale."""
+    state = derived_state(metadata, num_kv_heads, chunk_keys=chunk_keys)
+    device = k_pool.device
+    workspace = None
+    if state["workspace_bytes"]:
+        # One workspace per plan and stream: launches on one stream run in order, so the
+        # per-layer launches of a round reuse it (each merge finishes before the next
+        # layer's attention writes its partials).
+        ws_key = ("workspace", num_kv_heads, chunk_keys, stream)
+        workspace = per_meta.get(ws_key)
+        if workspace is None:
+            workspace = per_meta[ws_key] = torch.empty(state["workspace_bytes"], dtype=torch.uint8, device=device)
+    a = _lib.TreeAttentionArgs()
+    fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads, _device.status_word(device))
+    a.ancestor_words = state["ancestor_words"].data_ptr()
+    a.ancestor_words_per_row = state["words_per_row"]
     a.items = state["items_dev"].data_ptr()
     a.num_items = state["num_items"]
     a.groups = state["groups_dev"].data_ptr() if state["groups_dev"] is not None else None
@@ -194,8 +225,62 @@ def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> 
     a.num_partial_slots = state["num_partial_slots"]
     a.workspace = workspace.data_ptr() if workspace is not None else None
     a.workspace_bytes = state["workspace_bytes"]
-    a.status = _device.status_word(device).data_ptr()
-    _lib.check(lib.tv_tree_attention(ctypes.byref(a), _device.stream_handle(device)), "tree_attention")
+    a.device_counts = None
+    # Keep every buffer the block points at alive as long as the block.
+    return a, (state["ancestor_words"], state["items_dev"], state["groups_dev"], workspace)
+
+
+def _capture_id(stream: int) -> int:
+    capturing = ctypes.c_int32()
+    ident = ctypes.c_uint64()
+    lib = _lib.library()
+    _lib.check(lib.tv_stream_capture_info(stream, ctypes.byref(capturing), ctypes.byref(ident)),
+               "stream_capture_info")
+    if capturing.value != 1:
+        raise RuntimeError("tree attention: the stream's graph capture is not active")
+    return int(ident.value)
+
+
+def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int, chunk_keys: int,
+                     stream: int) -> torch.Tensor:
+    """Graph-capturable launch that follows the live device metadata on every replay."""
+    from .target_graph import GraphedTreeAttention
+
+    per_meta = _per_metadata(metadata)
+    key = ("graph", num_kv_heads, chunk_keys)
+    graphed = per_meta.get(key)
+    if graphed is None:
+        graphed = per_meta[key] = GraphedTreeAttention.for_signature(metadata, num_kv_heads, chunk_keys=chunk_keys)
+    capture = _capture_id(stream)
+    if graphed.prepared_capture != capture:
+        graphed.prepare(metadata)   # recorded once at the head of this graph's sequence
+        graphed.prepared_capture = capture
+    return graphed(q, k_pool, v_pool, metadata, scale, out, prepared=True)
+
+
+def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> torch.Tensor:
+    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    num_kv_heads = int(k_pool.shape[2])
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    if torch.cuda.is_current_stream_capturing():
+        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, chunk_keys, stream)
+    per_meta = _derived.get(id(metadata))
+    if per_meta is None:
+        per_meta = _per_metadata(metadata)
+    key = (num_kv_heads, chunk_keys, k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(), v_pool.stride(),
+           k_pool.shape[0], k_pool.dtype, stream)
+    entry = per_meta.get(key)
+    if entry is None:
+        entry = per_meta[key] = _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads, chunk_keys, stream)
+    a = _lib.TreeAttentionArgs.from_buffer_copy(entry[0])
+    a.q = q.data_ptr()
+    a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
+    a.out = out.data_ptr()
+    a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
+    a.out_dtype = _device.dtype_code(out.dtype)
+    a.scale = scale
+    _lib.check(_lib.library().tv_tree_attention(ctypes.byref(a), stream), "tree_attention")
     return out
 
 
@@ -209,17 +294,6 @@ def packed_tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.T
     """
     if backend not in _BACKENDS:
         raise ValueError("tree attention backend must be auto, reference, prefix or gqa")
-    if q.ndim != 3 or q.shape[0] != metadata.total_queries:
-        raise ValueError("packed queries do not match the metadata")
-    if k_pool.ndim != 4 or k_pool.shape != v_pool.shape or k_pool.shape[1] != metadata.block_size:
-        raise ValueError("packed K/V page geometry does not match metadata")
-    if (not q.is_cuda or q.device != k_pool.device or q.device != v_pool.device
-            or q.device != metadata.tree_slots.device):
-        raise ValueError("packed attention requires CUDA queries, KV and metadata on one device")
-    if q.stride(-1) != 1 or k_pool.shape[3] != q.shape[2]:
-        raise ValueError("unsupported packed query/KV head geometry")
-    if num_queries_per_kv <= 0 or q.shape[1] != k_pool.shape[2] * num_queries_per_kv:
-        raise ValueError("invalid packed GQA head grouping")
     if output_dtype not in (None, q.dtype, torch.float32):
         raise ValueError("output dtype must match input or be FP32 for qualification")
     dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
@@ -235,10 +309,10 @@ def packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_quer
 
 
 def packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *, output_dtype=None,
-                              query_tile=4, prefix_scalar=True, prune=True, fp32_probability=False, num_warps=4):
+                              query_tile=4, prefix_scalar=True, prune=True, fp32_probability=False):
     """Entry of tree_gqa.py:114-140; the tiling switches are accepted and fixed by the kernel."""
-    if isinstance(query_tile, bool) or query_tile not in (1, 2, 4):
-        raise ValueError("GQA query tile must be 1, 2 or 4")
+    if query_tile not in (1, 4) or isinstance(query_tile, bool):
+        raise ValueError("GQA query tile must be 1 or 4")
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("grouped Tensor Core tree attention requires BF16 or FP16")
     if num_queries_per_kv not in (1, 2, 4, 8, 16):

@@ -274,3 +274,63 @@ def test_plan_fills_its_rounds_of_work_items():
     prefixes = [int(x) for x in rng.integers(0, 16385, size=16)] + [int(x) for x in rng.integers(2048, 8193, size=32)]
     plan = make_plan(prefixes, [512] * 16 + [32] * 32, 8, 256, 256)
     assert plan["num_items"] == 1152 and plan["num_groups"] == 0
+
+
+def _capacity(lib, counts, kv_heads, block, cus, chunk, max_prefix):
+    info = _lib.PlanInfo()
+    arr = (ctypes.c_int32 * len(counts))(*counts)
+    _lib.check(lib.tv_tree_attention_plan_capacity(arr, len(counts), kv_heads, block, cus, chunk, max_prefix,
+                                                   ctypes.byref(info)), "capacity")
+    return info
+
+
+def _capacity_packed(lib, counts, kv_heads, block, cus, chunk, max_prefix):
+    info = _lib.PlanInfo()
+    _lib.check(lib.tv_tree_attention_plan_capacity_packed(sum(counts), len(counts), sum(n * n for n in counts),
+                                                          kv_heads, block, cus, chunk, max_prefix,
+                                                          ctypes.byref(info)), "capacity_packed")
+    return info
+
+
+def test_signature_capacity_covers_every_node_count_vector():
+    """The capture-mode capacity depends only on (requests, rows, sum of squares) and must
+    cover the exact capacity of every node-count vector with that signature: checked on
+    seeded random vectors and on pairs that share a signature."""
+    lib = _lib.library()
+    rng = np.random.default_rng(3)
+    vectors = [(12, 60, 72), (24, 36, 84), (1, 5, 6), (2, 3, 7), (64,) * 64, (1024,), (1, 1024), (33, 31)]
+    for _ in range(3000):
+        count = int(rng.integers(1, 9))
+        high = int(rng.choice([40, 130, 300, 1024]))
+        vectors.append(tuple(int(x) for x in rng.integers(1, high + 1, size=count)))
+    for counts in vectors:
+        for kv_heads, chunk in ((8, 0), (1, 0), (2, 0), (8, 2048)):
+            try:
+                exact = _capacity(lib, counts, kv_heads, 256, 256, chunk, 20000)
+            except ValueError:   # beyond the device planner: the signature bound must refuse too
+                with pytest.raises(ValueError):
+                    _capacity_packed(lib, counts, kv_heads, 256, 256, chunk, 20000)
+                continue
+            try:
+                packed = _capacity_packed(lib, counts, kv_heads, 256, 256, chunk, 20000)
+            except ValueError as error:   # the class bound may exceed the planner: a refusal, never a short plan
+                assert "exceed" in str(error)
+                continue
+            assert packed.num_items >= exact.num_items, (counts, kv_heads, chunk)
+            assert packed.num_groups >= exact.num_groups, (counts, kv_heads, chunk)
+            assert packed.num_partial_slots >= exact.num_partial_slots, (counts, kv_heads, chunk)
+            assert packed.ancestor_words_per_row >= exact.ancestor_words_per_row, (counts, kv_heads, chunk)
+            assert packed.workspace_bytes >= exact.workspace_bytes, (counts, kv_heads, chunk)
+    # (12, 60, 72) and (24, 36, 84) share a signature; so do (1, 5, 6) and (2, 3, 7).
+    a = _capacity_packed(lib, (12, 60, 72), 8, 256, 256, 0, 8192)
+    b = _capacity_packed(lib, (24, 36, 84), 8, 256, 256, 0, 8192)
+    assert (a.num_items, a.num_groups, a.ancestor_words_per_row) == (b.num_items, b.num_groups,
+                                                                      b.ancestor_words_per_row)
+    info = _lib.PlanInfo()
+    assert lib.tv_tree_attention_plan_capacity_packed(2, 3, 0, 8, 256, 256, 0, 100, ctypes.byref(info)) \
+        == _lib.TV_ERR_INVALID   # fewer rows than requests
+
+
+def test_stream_capture_info_rejects_null_outputs():
+    lib = _lib.library()
+    assert lib.tv_stream_capture_info(None, None, None) == _lib.TV_ERR_INVALID

@@ -17,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_helpers import assert_within_gate, oracle_rows
 from jetspec_amd import (PackedTreeMetadata, _device, _lib, packed_tree_attention, read_and_clear_status,
                          rope_scatter_prevalidated, workloads)
 from jetspec_amd.paged_backend import make_plan
@@ -129,6 +130,9 @@ def test_graphed_attention_equals_eager(name):
     attn(q, pool[0], pool[1], meta, 128 ** -0.5, out)
     assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
     assert read_and_clear_status(DEV) == 0
+    reference = oracle_rows(q, pool[0], pool[1], meta, 128 ** -0.5, list(range(meta.num_requests)),
+                            rows_per_request=8)
+    assert_within_gate(out, reference, f"graphed {name}")
 
 
 def verify_round(seed, counts, pages, max_prefix):
@@ -161,13 +165,14 @@ def verify_round(seed, counts, pages, max_prefix):
 
 
 def eager_round(kv_pool, cache, meta, positions, q, k, v):
-    outs = []
+    outs, rotations = [], []
     for layer in range(q.shape[0]):
         rotated = torch.empty_like(q[layer])
         rope_scatter_prevalidated(q[layer], k[layer], v[layer], positions, cache, kv_pool[0, layer],
                                   kv_pool[1, layer], meta.tree_slots, rotated)
+        rotations.append(rotated)
         outs.append(packed_tree_attention(rotated, kv_pool[0, layer], kv_pool[1, layer], meta, 128 ** -0.5, 4))
-    return torch.stack(outs)
+    return torch.stack(outs), torch.stack(rotations)
 
 
 def test_verify_graph_replays_match_eager():
@@ -182,13 +187,18 @@ def test_verify_graph_replays_match_eager():
     for round_index in range(4):
         meta, positions, q, k, v = verify_round(100 + round_index, counts, pages, max_prefix)
         reference_pool = pool.clone()
-        expected = eager_round(reference_pool, cache, meta, positions, q, k, v)
+        expected, rotated = eager_round(reference_pool, cache, meta, positions, q, k, v)
         torch.cuda.synchronize()
         got = graph.verify(q, k, v, positions, meta).clone()
         torch.cuda.synchronize()
         print(f"[graph] round {round_index}: prefixes {meta.prefix_lengths} {graph.snapshot()}", flush=True)
         assert torch.equal(got.view(torch.int16), expected.view(torch.int16)), f"round {round_index} output"
         assert torch.equal(pool.view(torch.int16), reference_pool.view(torch.int16)), f"round {round_index} pool"
+        # The replay against the fp64 oracle on the same rotated queries and pool rows.
+        for layer in range(q.shape[0]):
+            reference = oracle_rows(rotated[layer], pool[0, layer], pool[1, layer], meta, 128 ** -0.5,
+                                    list(range(meta.num_requests)))
+            assert_within_gate(got[layer], reference, f"graph replay round {round_index} layer {layer}")
         # Eager work between replays (a different stream state and allocator traffic).
         torch.randn(1 << 20, device=DEV).sum().item()
     assert graph.captures == 1 and graph.replays == 4
