@@ -63,14 +63,27 @@ def parse_args():
     return parser.parse_args()
 
 
-def traffic_bytes(config: int):
-    """HBM bytes per attention launch measured with rocprofv3 PMC counters (committed summary)."""
+def source_digest(paths) -> str:
+    """sha256 over the named source files (relative to the repository root), in order."""
+    import hashlib
+
+    digest = hashlib.sha256()
+    for rel in paths:
+        digest.update((ROOT / rel).read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def traffic_bytes(key: str):
+    """HBM bytes per launch measured with rocprofv3 PMC counters (committed summary), or None
+    when the kernel sources changed since that measurement (the entry's `source_sha` no longer
+    matches), so a stale count is never reported."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
-    data = json.loads(path.read_text())
-    entry = data.get(f"cfg{config}")
-    return None if entry is None else entry.get("hbm_bytes_per_launch")
+    entry = json.loads(path.read_text()).get(key)
+    if entry is None or "sources" not in entry or entry.get("source_sha") != source_digest(entry["sources"]):
+        return None
+    return entry.get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(batch, requests: int) -> dict:
@@ -100,7 +113,10 @@ def cpu_baseline(batch, requests: int) -> dict:
     sub = PackedTreeMetadata.build([meta.prefix_lengths[r] for r in chosen],
                                    [[remap[p] for p in meta.block_tables_host[r]] for r in chosen],
                                    slots, ancestors, block)
-    threads = torch.get_num_threads()
+    # Every host core of the box (torch.set_num_threads(os.cpu_count()), the CPU baseline plan).
+    previous = torch.get_num_threads()
+    threads = os.cpu_count() or previous
+    torch.set_num_threads(threads)
 
     def step():
         cpu_path.append(k_pool, v_pool, new_k, new_v, sub.tree_slots)
@@ -113,7 +129,13 @@ def cpu_baseline(batch, requests: int) -> dict:
         step()
         samples.append(time.perf_counter() - t0)
     seconds = statistics.median(samples)
+    torch.set_num_threads(previous)
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = threads
     return {"value": sub.total_queries / seconds, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpus_in_affinity_mask": affinity,
             "sample": f"requests 0..{len(chosen) - 1} of the same batch ({sub.total_queries} tree rows, "
                       f"{sum(sub.prefix_lengths)} prefix tokens); append + bf16 SDPA over page-table-gathered K/V; "
                       f"median of 3 after 1 warmup, samples_s={[round(s, 3) for s in samples]}"}
@@ -348,7 +370,7 @@ def run_verify(args, torch):
                      "peak": MFMA_BF16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
                      "unit": "TFLOP/s" if mfma_bound else "GB/s",
                      "frac": tflops / MFMA_BF16_PEAK_TFLOPS if mfma_bound else achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_bytes(args.config) if args.kv_heads == 8 else None,
+                     "traffic": traffic_bytes(f"cfg{args.config}") if args.kv_heads == 8 else None,
                      "kernel": "tree_attention_kernel", "kernel_ms": attn_ms, "algorithmic_bytes": algo_bytes,
                      "algorithmic_flops": algo_flops, "achieved_gbs": achieved, "achieved_tflops": tflops,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
@@ -405,7 +427,7 @@ def run_commit(args, torch):
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
             "config": {"workload": WORKLOADS[3], "accepted_rows": rows, "pool_pages": batch.info["pages"]},
             "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes(3), "kernel_ms": ms,
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_bytes("cfg3"), "kernel_ms": ms,
                          "algorithmic_bytes": algo, "measured_copy_gbs": probe["gbs"],
                          "frac_of_measured_copy": achieved / probe["gbs"]}}
 

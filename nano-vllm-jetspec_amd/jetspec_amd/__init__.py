@@ -10,14 +10,15 @@ Drop-in operators (same names, arguments and errors as the reference):
 Each device operator is a hand-written gfx950 HIP kernel in libtreeverify.so.
 """
 from .packed_metadata import PackedTreeMetadata
-from .paged_backend import (
-    packed_tree_attention,
-    packed_tree_attention_gqa,
+from .paged_backend import packed_tree_attention, paged_tree_attention
+from .tree_attention import packed_tree_attention_reference, packed_tree_attention_register_tuned
+from .tree_dot import packed_tree_attention_dot
+from .tree_gqa import packed_tree_attention_gqa
+from .tree_prefix import (
+    packed_tree_attention_prefix,
     packed_tree_attention_prefix_prevalidated,
+    packed_tree_attention_prefix_single_loop,
     packed_tree_attention_prefix_split_exact,
-    packed_tree_attention_reference,
-    packed_tree_attention_register_tuned,
-    paged_tree_attention,
 )
 from .attention import store_kvcache
 from .tree_fusion import rope_scatter, rope_scatter_prevalidated
@@ -30,7 +31,10 @@ from ._lib import library
 __all__ = [
     "PackedTreeMetadata",
     "packed_tree_attention",
+    "packed_tree_attention_dot",
     "packed_tree_attention_gqa",
+    "packed_tree_attention_prefix",
+    "packed_tree_attention_prefix_single_loop",
     "packed_tree_attention_prefix_prevalidated",
     "packed_tree_attention_prefix_split_exact",
     "packed_tree_attention_reference",

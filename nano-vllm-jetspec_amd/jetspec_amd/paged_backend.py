@@ -284,65 +284,40 @@ def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> 
     return out
 
 
+def _launch_new(q, k_pool, v_pool, metadata, scale, dtype) -> torch.Tensor:
+    """Launch into a new output of `dtype` (the checked entries' allocation, tree_attention.py:36)."""
+    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device))
+
+
 def packed_tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, metadata, scale: float,
                           num_queries_per_kv: int, *, backend: str = "auto",
                           output_dtype: torch.dtype | None = None, chunk_keys: int = 0) -> torch.Tensor:
     """One ragged launch with independent request/ancestor visibility (paged_backend.py:240-306).
 
-    ``backend`` accepts the reference's names; all select the one HIP kernel.
-    ``chunk_keys`` (extension, default automatic) fixes the prefix split length.
+    ``backend`` takes the reference's names and dispatches to the same-named entries
+    (tree_gqa, tree_attention, tree_prefix modules of this package), as the reference
+    does; every entry runs the one HIP kernel.  ``chunk_keys`` (extension, default
+    automatic) fixes the prefix split length.
     """
     if backend not in _BACKENDS:
         raise ValueError("tree attention backend must be auto, reference, prefix or gqa")
     if output_dtype not in (None, q.dtype, torch.float32):
         raise ValueError("output dtype must match input or be FP32 for qualification")
+    if backend == "gqa":
+        from .tree_gqa import packed_tree_attention_gqa
+        return packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
+                                         output_dtype=output_dtype)
+    if backend == "reference":
+        from .tree_attention import packed_tree_attention_reference
+        return packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
+                                               output_dtype=output_dtype)
+    if backend == "prefix":
+        from .tree_prefix import packed_tree_attention_prefix_split_exact
+        return packed_tree_attention_prefix_split_exact(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
+                                                        output_dtype=output_dtype, num_warps=4)
     dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
     out = torch.empty(q.shape, dtype=dtype, device=q.device)
     return _launch(q, k_pool, v_pool, metadata, scale, out, chunk_keys=chunk_keys)
-
-
-def packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,
-                                    output_dtype=None):
-    """Entry of tree_attention.py:40-62 (explicit FP32 output supported)."""
-    dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
-    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device))
-
-
-def packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *, output_dtype=None,
-                              query_tile=4, prefix_scalar=True, prune=True, fp32_probability=False):
-    """Entry of tree_gqa.py:114-140; the tiling switches are accepted and fixed by the kernel."""
-    if query_tile not in (1, 4) or isinstance(query_tile, bool):
-        raise ValueError("GQA query tile must be 1 or 4")
-    if q.dtype not in (torch.bfloat16, torch.float16):
-        raise ValueError("grouped Tensor Core tree attention requires BF16 or FP16")
-    if num_queries_per_kv not in (1, 2, 4, 8, 16):
-        raise ValueError("grouped tree attention requires power-of-two GQA <=16")
-    dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
-    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device))
-
-
-def packed_tree_attention_register_tuned(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,
-                                         output_dtype=None, maxnreg=96):
-    """Entry of tree_attention.py:170-203; the register cap is a CUDA knob with no meaning here."""
-    if isinstance(maxnreg, bool) or maxnreg not in (64, 80, 96, 112, 128):
-        raise ValueError("maxnreg must be 64, 80, 96, 112 or 128")
-    return packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
-                                           output_dtype=output_dtype)
-
-
-def packed_tree_attention_prefix_split_exact(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,
-                                             output_dtype=None, num_warps=4):
-    """Entry of tree_prefix.py:444-463."""
-    if isinstance(num_warps, bool) or num_warps not in (4, 8, 16):
-        raise ValueError("num_warps must be 4, 8 or 16")
-    return packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
-                                           output_dtype=output_dtype)
-
-
-def packed_tree_attention_prefix_prevalidated(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, out, *,
-                                              num_warps=4):
-    """Launch-only serving entry (tree_prefix.py:466-492): caller validated and allocated `out`."""
-    return _launch(q, k_pool, v_pool, metadata, scale, out)
 
 
 def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_k, qq_bias, scale,

@@ -16,6 +16,8 @@ Contents (each restates the cited reference code):
   accept_walk           speculative/jetspec/serving_ops.py:55-90
   truncate_accepted     speculative/jetspec/batch_runtime.py:636-655 (per request)
   argmax_flip_witness   benchmarks/jetspec_numeric_oracles.py:171-217
+  numerical_metrics     benchmarks/jetspec_numeric_oracles.py:108-168 (max-abs, rel-RMS,
+                        the fixed FP32 bound and the bf16-ULP diagnostics)
   rope_scatter_hf       speculative/jetspec/tree_fusion.py:20-82 and the eager HF RoPE
                         + scatter it replaces, models/qwen3.py:241-258 (numpy, exact
                         bf16 round-to-nearest-even on uint16 bit patterns)
@@ -358,6 +360,73 @@ def argmax_flip_witness(actual: np.ndarray, reference: np.ndarray) -> dict:
         flips += int(flipped)
         violations += int(flipped and not consistent)
     return {"rows_checked": a.shape[0], "argmax_flips": flips, "large_margin_violations": violations}
+
+
+FP32_ATTENTION_BOUND = 1e-4   # benchmarks/jetspec_numeric_oracles.py:21
+
+
+def round_f64_to_bf16(values: np.ndarray) -> np.ndarray:
+    """float64 -> bf16 value as float64, the way the reference's ``.to(torch.bfloat16)`` of a
+    float64 tensor rounds: to the nearest float32 first, then to the nearest bf16 (ties to
+    even at both steps)."""
+    with np.errstate(over="ignore"):
+        single = np.asarray(values, dtype=np.float64).astype(np.float32)
+    return bf16_bits_to_f32(f32_to_bf16_bits(single)).astype(np.float64)
+
+
+def bf16_ulp(rounded: np.ndarray) -> np.ndarray:
+    """The larger spacing between a bf16 value and its two bf16 neighbours: 2^(e-8) for a
+    normal value m * 2^e (the spacing below a power of two is the smaller one), and the
+    smallest bf16 subnormal 2^-133 at zero."""
+    r = np.asarray(rounded, dtype=np.float64)
+    _, exponent = np.frexp(r)
+    return np.where(r == 0, 2.0 ** -133, np.ldexp(1.0, exponent - 8))
+
+
+def numerical_metrics(actual, reference, *, bound_scale: float = FP32_ATTENTION_BOUND,
+                      bf16_output: bool | None = None) -> dict:
+    """The reference's numerical_metrics (jetspec_numeric_oracles.py:108-168) in float64.
+
+    within_fixed_bound = max-abs <= bound_scale * max(1, |reference|_max) and relative RMS
+    (RMS of the difference over RMS of the reference) <= bound_scale; the bound applies to
+    FP32 output before bf16 rounding.  The bf16 diagnostics measure errors in units of the
+    larger neighbour spacing around the reference's nearest bf16 value.
+    """
+    a_in = np.asarray(actual)
+    left = np.asarray(actual, dtype=np.float64)
+    right = np.asarray(reference, dtype=np.float64)
+    if left.shape != right.shape or left.size == 0:
+        raise ValueError("metric tensors must have equal nonempty shapes")
+    if not math.isfinite(float(bound_scale)) or float(bound_scale) <= 0:
+        raise ValueError("bound scale must be finite and positive")
+    quantized = (str(a_in.dtype) == "bfloat16") if bf16_output is None else bool(bf16_output)
+    difference = left - right
+    max_abs = float(np.abs(difference).max())
+    rms_error = float(np.sqrt(np.mean(difference ** 2)))
+    reference_rms = float(np.sqrt(np.mean(right ** 2)))
+    reference_absmax = float(np.abs(right).max())
+    if reference_rms:
+        relative_rms = rms_error / reference_rms
+    else:
+        relative_rms = 0.0 if rms_error == 0.0 else float("inf")
+    max_abs_bound = float(bound_scale) * max(1.0, reference_absmax)
+    rounded = round_f64_to_bf16(right)
+    ulp = bf16_ulp(rounded)
+    bf16_difference = round_f64_to_bf16(left) - rounded
+    return {
+        "elements": int(left.size), "max_abs_error": max_abs, "rms_error": rms_error,
+        "relative_rms_error": relative_rms, "reference_absmax": reference_absmax, "reference_rms": reference_rms,
+        "max_abs_bound": max_abs_bound, "relative_rms_bound": float(bound_scale),
+        "within_fixed_bound": max_abs <= max_abs_bound and relative_rms <= float(bound_scale),
+        "fixed_bound_applicable": not quantized,
+        "bf16_quantization": {
+            "actual_output_is_bf16": quantized,
+            "max_error_in_bf16_ulps": float((np.abs(difference) / ulp).max()),
+            "max_distance_from_nearest_bf16_in_ulps": float((np.abs(bf16_difference) / ulp).max()),
+            "nearest_bf16_unequal_elements": int(np.count_nonzero(bf16_difference)),
+            "nearest_rounding_max_abs_error": float(np.abs(rounded - right).max()),
+        },
+    }
 
 
 # --------------------------------------------------------------------------- HF-order RoPE + scatter

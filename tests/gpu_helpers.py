@@ -77,9 +77,18 @@ def errors(actual: torch.Tensor, expected: dict) -> tuple[float, float]:
     return float(flat.max()), float(flat.mean())
 
 
+def metrics(actual: torch.Tensor, expected: dict) -> dict:
+    """The reference's numerical_metrics (oracle restatement) over the compared rows."""
+    got = actual.float().cpu().numpy()
+    left = np.concatenate([got[rows].reshape(-1) for rows, _ in expected.values()])
+    right = np.concatenate([ref.reshape(-1) for _, ref in expected.values()])
+    return oracle.numerical_metrics(left, right, bf16_output=actual.dtype == torch.bfloat16)
+
+
 def assert_within_gate(actual: torch.Tensor, expected: dict, label: str, max_abs=MAX_ABS, mean_abs=MEAN_ABS):
     mx, mean = errors(actual, expected)
-    print(f"[{label}] max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    rel = metrics(actual, expected)["relative_rms_error"] if np.isfinite(mx) else float("nan")
+    print(f"[{label}] max-abs {mx:.3e} mean-abs {mean:.3e} rel-RMS {100 * rel:.3f}%", flush=True)
     assert np.isfinite(mx), f"{label}: non-finite output"
     assert mx <= max_abs, f"{label}: max-abs {mx} > {max_abs}"
     assert mean <= mean_abs, f"{label}: mean-abs {mean} > {mean_abs}"

@@ -238,3 +238,23 @@ def test_truncation_bad_requests_and_commit_chain():
     assert not bad.any() and live_paths.numel() == n
     assert src.tolist() == esrc.tolist() and dst.tolist() == edst.tolist()
     assert read_and_clear_status(DEV) == 0
+
+
+@pytest.mark.parametrize("max_depth,path_nodes,correction", [(15, 16, 26), (3, 4, 14), (0, 1, 11), (25, 20, 99)])
+def test_device_depth_cap_closed_form(max_depth, path_nodes, correction):
+    """serving_ops.py:78 on the device: a 20-node chain whose every node's argmax is its child's
+    token gives nodes 0..min(max_depth, 19) and the last node's argmax as the correction."""
+    nodes, vocab = 20, 128
+    tokens = torch.tensor([10 + i for i in range(nodes)], device=DEV)
+    parents = torch.tensor([-1] + list(range(nodes - 1)), dtype=torch.int32, device=DEV)
+    depths = torch.arange(nodes, device=DEV)
+    logits = torch.zeros(nodes, vocab, device=DEV)
+    for i in range(nodes - 1):
+        logits[i, 10 + i + 1] = 5.0
+    logits[nodes - 1, 99] = 5.0
+    cu = torch.tensor([0, nodes], dtype=torch.int32, device=DEV)
+    _, paths, lengths, corrections = accept_batch_device(logits, tokens, parents, depths, cu, max_depth)
+    assert paths[0, :path_nodes].tolist() == list(range(path_nodes))
+    assert (paths[0, path_nodes:] == -1).all()
+    assert int(lengths[0]) == path_nodes - 1 and int(corrections[0]) == correction
+    assert read_and_clear_status(DEV) == 0

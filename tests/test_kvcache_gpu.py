@@ -125,29 +125,30 @@ def test_commit_contract():
     assert torch.equal(pool.view(torch.int16), before.view(torch.int16)), "an invalid map must not write"
 
 
-def test_config3_commit_full_size_properties():
+def test_config3_commit_full_size_byte_exact():
+    """Config 3 at full size (36 layers, 64 requests): the whole pool after the commit equals,
+    byte for byte and one (K/V, layer) plane at a time, a copy of the pool before it to which
+    the index-copy closed form of state.py:80-85 (gather the source rows, then scatter them to
+    the destinations) was applied."""
     batch = workloads.config3(DEV)
     pool, src, dst = batch.kv_pool, batch.source, batch.destination
     print(f"[cfg3] pool {tuple(pool.shape)} rows {src.numel()} "
           f"payload {2 * pool.shape[1] * src.numel() * 2048 / 1e6:.1f} MB", flush=True)
     block = pool.shape[3]
-    flat = pool.view(2, pool.shape[1], -1, 8, 128)
-    expected_rows = flat[:, :, src].clone()
-    dst_set = set(dst.tolist())
-    assert not dst_set & set(src.tolist())
-    # checksum of every slot row before the commit, per (kv, layer)
-    def row_sums():
-        return torch.stack([flat[kv, layer].view(torch.int16).view(-1, 1024).to(torch.int32).sum(1)
-                            for kv in range(2) for layer in range(pool.shape[1])])
-    before = row_sums()
+    expected = pool.clone()
+    assert not set(dst.tolist()) & set(src.tolist())
     payload = copy_accepted_kv(pool, src, dst, block)
     torch.cuda.synchronize()
     assert payload == 2 * pool.shape[1] * src.numel() * 8 * 128 * 2
-    assert bool(torch.equal(flat[:, :, dst].view(torch.int16), expected_rows.view(torch.int16)))
-    after = row_sums()
-    untouched = torch.ones(before.shape[1], dtype=torch.bool, device=DEV)
-    untouched[dst] = False
-    assert bool(torch.equal(before[:, untouched], after[:, untouched]))
+    flat = pool.view(2, pool.shape[1], -1, 8 * 128).view(torch.int16)
+    want = expected.view(2, pool.shape[1], -1, 8 * 128).view(torch.int16)
+    for kv in range(2):
+        for layer in range(pool.shape[1]):
+            plane = want[kv, layer]
+            rows = plane[src].clone()
+            plane[dst] = rows
+            assert bool(torch.equal(flat[kv, layer], plane)), f"plane kv={kv} layer={layer} differs"
+    del expected
     assert read_and_clear_status(DEV) == 0
 
 

@@ -16,6 +16,7 @@ import json
 from pathlib import Path
 
 import numpy as np
+import torch
 import pytest
 
 import oracle
@@ -349,3 +350,48 @@ def test_truncate_oracle_reference_kats():
     assert oracle.truncate_accepted([63, 2], [0, 3], 16, False, {63})["limit"] == 1
     with pytest.raises(ValueError):
         oracle.truncate_accepted([1, 2], [0], 4, False, set())
+
+
+# ---------------------------------------------------------------- numerical_metrics
+def test_numerical_metrics_closed_forms():
+    """jetspec_numeric_oracles.py:108-168 restated: identity, a constant offset (every error
+    statistic known in closed form), and the fixed bound's conjunction on both sides."""
+    rng = np.random.default_rng(11)
+    ref = rng.standard_normal((4, 32, 128))
+    same = oracle.numerical_metrics(ref.copy(), ref)
+    assert same["max_abs_error"] == 0 and same["rms_error"] == 0 and same["relative_rms_error"] == 0
+    assert same["within_fixed_bound"] and same["fixed_bound_applicable"]
+    ref_rms = float(np.sqrt(np.mean(ref ** 2)))
+    for c in (1e-6, 5e-5, 3e-3):
+        m = oracle.numerical_metrics(ref + c, ref)
+        assert m["max_abs_error"] == pytest.approx(c, rel=1e-9)
+        assert m["rms_error"] == pytest.approx(c, rel=1e-9)
+        assert m["relative_rms_error"] == pytest.approx(c / ref_rms, rel=1e-9)   # over the REFERENCE's RMS
+        bound = 1e-4 * max(1.0, float(np.abs(ref).max()))
+        assert m["within_fixed_bound"] == (c <= bound and c / ref_rms <= 1e-4)
+    # Scaling the actual alone must not change the denominator.
+    m = oracle.numerical_metrics(2 * ref, ref)
+    assert m["relative_rms_error"] == pytest.approx(1.0, rel=1e-12)
+    assert oracle.numerical_metrics(np.zeros(3), np.zeros(3))["relative_rms_error"] == 0.0
+    assert oracle.numerical_metrics(np.ones(3), np.zeros(3))["relative_rms_error"] == float("inf")
+    with pytest.raises(ValueError):
+        oracle.numerical_metrics(np.zeros(3), np.zeros(4))
+
+
+def test_numerical_metrics_bf16_ulps_against_torch():
+    """The bf16 diagnostics: the nearest bf16 value is torch's own float64 -> bfloat16
+    conversion, the ULP is the larger of torch.nextafter's two neighbour spacings, and the
+    hand-computed cases 1.0 (ULP 2^-7), 0.75 (2^-8) and 3.0 (2^-6) hold."""
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal(50000) * np.exp(rng.uniform(-30, 30, 50000))
+    t = torch.from_numpy(x).to(torch.bfloat16)
+    assert np.array_equal(oracle.round_f64_to_bf16(x), t.double().numpy())
+    up = torch.nextafter(t, torch.full_like(t, float("inf"))).double() - t.double()
+    down = t.double() - torch.nextafter(t, torch.full_like(t, float("-inf"))).double()
+    assert np.array_equal(oracle.bf16_ulp(t.double().numpy()), torch.maximum(up, down).numpy())
+    ref = np.array([1.0, 0.75, 3.0])
+    assert np.array_equal(oracle.bf16_ulp(ref), [2.0 ** -7, 2.0 ** -8, 2.0 ** -6])
+    m = oracle.numerical_metrics(ref + np.array([2.0 ** -7, 0, 0]), ref, bf16_output=True)
+    q = m["bf16_quantization"]
+    assert q["max_error_in_bf16_ulps"] == 1.0 and q["nearest_bf16_unequal_elements"] == 1
+    assert q["actual_output_is_bf16"] and not m["fixed_bound_applicable"]

@@ -72,3 +72,29 @@ def test_device_operators_reject_cpu_tensors():
     with pytest.raises(ValueError, match="no CPU path"):
         truncate_accepted(torch.zeros((1, 2), dtype=torch.int32), i32[:1], torch.zeros(1, dtype=torch.int64),
                           i32[:1], i32, i32[:1], torch.zeros(1, dtype=torch.bool), [2])
+
+
+def _chain_case(nodes: int, vocab: int = 128):
+    """A chain whose every node's argmax is its child's token: the walk accepts until the cap."""
+    tokens = [10 + i for i in range(nodes)]
+    parents = [-1] + list(range(nodes - 1))
+    logits = torch.zeros(nodes, vocab)
+    for i in range(nodes - 1):
+        logits[i, tokens[i + 1]] = 5.0
+    logits[nodes - 1, 99] = 5.0
+    return tokens, parents, logits
+
+
+@pytest.mark.parametrize("max_depth,path_nodes,correction", [(15, 16, 26), (3, 4, 14), (0, 1, 11), (25, 20, 99)])
+def test_depth_cap_closed_form(max_depth, path_nodes, correction):
+    """serving_ops.py:78: the walk keeps at most max_depth + 1 path nodes.  On a 20-node chain
+    where every node's argmax names its child, the path is nodes 0..min(max_depth, 19) and the
+    correction is the argmax of its last node (token 10 + last + 1, or 99 at the chain's end)."""
+    tokens, parents, logits = _chain_case(20)
+    tree = SimpleNamespace(num_nodes=20, host_token_ids=tokens, host_depths=list(range(20)),
+                           child_maps=oracle.child_maps(tokens, parents), parents=parents)
+    result = accept_batch(logits, [tree], [0, 20], max_depth)[0]
+    assert result["path"] == list(range(path_nodes))
+    assert result["accepted_length"] == path_nodes - 1
+    assert result["correction"] == correction
+    assert result["outputs"] == tokens[1:path_nodes] + [correction]
