@@ -413,6 +413,22 @@ typedef struct tv_tree_attention_args {
  */
 int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
 
+/*
+ * Allocation-free variant of tv_tree_attention.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under graph capture, tight serving
+ * loops, harnesses that forbid allocation).  Same arguments, except that `workspace` and
+ * `workspace_bytes` are ignored: split prefixes keep their partial results in a scratch
+ * array built into the library, one per device, of tv_tree_attention_noalloc_max_workspace()
+ * bytes (64 MiB: 500 partial slots, about two rounds of work items on 256 CUs), held until
+ * the process ends.  A plan whose partial slots need more returns TV_ERR_CAPACITY and
+ * launches nothing.  Every call on one device shares that device's scratch, so calls that
+ * overlap on one device (concurrent streams) race; calls ordered on one stream do not.
+ * No hipMalloc, hipFree or allocating library routine is called.
+ */
+int tv_tree_attention_noalloc(const tv_tree_attention_args* args, void* stream);
+
+int64_t tv_tree_attention_noalloc_max_workspace(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,6 +47,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "tv_internal.h"
 
 namespace tv {
@@ -985,8 +987,17 @@ extern "C" int tv_pack_ancestor_words(const float* qq_bias, const int64_t* qq_bi
     return check_launch("pack_ancestor_words");
 }
 
-extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) {
-    clear_error();
+// Scratch of the allocation-free entry (tv_tree_attention_noalloc): one array per device,
+// held until the process ends.  Its host-side name is only a stand-in; the device address
+// comes from hipGetSymbolAddress, taken once per device with that device current.
+constexpr int64_t kScratchBytes = int64_t{64} << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+
+// Validates `a` and enqueues the attention (and the merge of split prefixes) with the
+// partial-result workspace that `a` names.
+int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     if (!a) return fail(TV_ERR_INVALID, "tree_attention: null args");
     if (a->head_dim != kHeadDim) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: head_dim %d (implemented: 128)", a->head_dim);
@@ -1105,4 +1116,66 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
         }
     }
     return check_launch("tree_attention");
+}
+
+// Split-K workspace bytes a plan with `slots` partial slots needs (partial O, then (max, sum)).
+int64_t workspace_need(int64_t slots) {
+    if (slots <= 0) return 0;
+    const int64_t o_span = (slots * kRowsPerItem * kHeadDim * 4 + 255) / 256 * 256;
+    return o_span + (slots * kRowsPerItem * 8 + 255) / 256 * 256;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(void** out) {
+    int device = -1;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return fail(TV_ERR_LAUNCH, "tree_attention_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+    if (device < 0 || device >= kMaxDevices) {
+        return fail(TV_ERR_UNSUPPORTED, "tree_attention_noalloc: device %d beyond %d", device, kMaxDevices);
+    }
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr) {
+            return fail(TV_ERR_LAUNCH, "tree_attention_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(err));
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return TV_OK;
+}
+
+}  // namespace
+
+extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) {
+    clear_error();
+    return launch_tree_attention(a, stream);
+}
+
+extern "C" int64_t tv_tree_attention_noalloc_max_workspace(void) { return kScratchBytes; }
+
+extern "C" int tv_tree_attention_noalloc(const tv_tree_attention_args* a, void* stream) {
+    clear_error();
+    if (!a) return fail(TV_ERR_INVALID, "tree_attention_noalloc: null args");
+    if (a->num_partial_slots < 0) return fail(TV_ERR_INVALID, "tree_attention_noalloc: invalid counts");
+    const int64_t need = workspace_need(a->num_partial_slots);
+    if (need > kScratchBytes) {
+        return fail(TV_ERR_CAPACITY,
+                    "tree_attention_noalloc: the plan's %d partial slots need %lld workspace bytes, above the "
+                    "%lld-byte built-in scratch; use tv_tree_attention with a caller workspace",
+                    a->num_partial_slots, (long long)need, (long long)kScratchBytes);
+    }
+    tv_tree_attention_args local = *a;
+    local.workspace = nullptr;
+    local.workspace_bytes = 0;
+    if (need > 0) {
+        const int code = scratch_for_current_device(&local.workspace);
+        if (code != TV_OK) return code;
+        local.workspace_bytes = kScratchBytes;
+    }
+    return launch_tree_attention(&local, stream);
 }

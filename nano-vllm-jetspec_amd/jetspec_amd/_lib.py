@@ -53,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "tv_tree_attention_plan_device",
     "tv_tree_attention_plan_capacity_packed",
     "tv_stream_capture_info",
+    "tv_tree_attention_noalloc",
+    "tv_tree_attention_noalloc_max_workspace",
 )
 
 
@@ -163,6 +165,10 @@ def _declare(lib: ctypes.CDLL) -> None:
                                            c_int32, c_void_p, c_void_p, c_void_p]
     lib.tv_tree_attention.restype = c_int32
     lib.tv_tree_attention.argtypes = [POINTER(TreeAttentionArgs), c_void_p]
+    lib.tv_tree_attention_noalloc.restype = c_int32
+    lib.tv_tree_attention_noalloc.argtypes = [POINTER(TreeAttentionArgs), c_void_p]
+    lib.tv_tree_attention_noalloc_max_workspace.restype = c_int64
+    lib.tv_tree_attention_noalloc_max_workspace.argtypes = []
     lib.tv_sizeof_rope_scatter_args.restype = c_int64
     lib.tv_sizeof_rope_scatter_args.argtypes = []
     lib.tv_rope_scatter.restype = c_int32
