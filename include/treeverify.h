@@ -271,6 +271,18 @@ int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_
                            tv_attention_plan_info* info);
 
 /*
+ * The plan of a slot-addressed launch (tv_tree_attention_args.prefix_slots set): the same
+ * items, with every prefix chunk at most 2048 keys (the keys' slots are cached per work
+ * item) and no page-size constraint.  Replaces the grid of the legacy single-request
+ * kernel, paged_backend.py:343-348.
+ */
+int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
+                                 int32_t num_requests, int32_t num_kv_heads,
+                                 int32_t num_compute_units, int32_t chunk_keys,
+                                 int32_t* items_host, int32_t* groups_host,
+                                 tv_attention_plan_info* info);
+
+/*
  * Device-side planner: the same items and groups as tv_tree_attention_plan, item for
  * item, computed on the device from device prefix_lens / node_counts, so a launch
  * sequence keeps fixed grids while prefix lengths change (HIP graph replay, the
@@ -399,6 +411,21 @@ typedef struct tv_tree_attention_args {
      * When set, num_items / num_groups / num_partial_slots are launch capacities and the
      * kernels read the live counts from here (a graph-capturable launch). */
     const int32_t* device_counts;
+    /* optional: slot addressing of the prefix, the legacy single-request form of
+     * paged_backend.py:20-113 (a logical slot per key instead of a page table).  When set,
+     * prefix key k of request r is read at slot prefix_slots[r * prefix_slots_stride + k]
+     * (int64 if prefix_slots_is_int64, else int32; page slot / block_size, offset
+     * slot % block_size), block_tables is not read, block_size may be any positive value,
+     * the plan must come from tv_tree_attention_plan_slots, and exact_probabilities must
+     * be set (the legacy kernel is an FP32 one). */
+    const void* prefix_slots;
+    int64_t prefix_slots_stride;
+    int32_t prefix_slots_is_int64;
+    /* nonzero: keep each probability to ~2^-17 relative in the P.V product (two MFMAs:
+     * its operand-type rounding and the rounding of the remainder) and sum them in fp32,
+     * for the reference's FP32 entries (tree_attention.py:1-10, paged_backend.py:248-256:
+     * "never BF16 probabilities"); zero: one operand-type rounding (tree_gqa.py:102-105). */
+    int32_t exact_probabilities;
 } tv_tree_attention_args;
 
 /*
@@ -409,7 +436,7 @@ typedef struct tv_tree_attention_args {
  * fp32 accumulation and online softmax, probabilities rounded to the operand
  * type for the P.V product (tree_gqa.py:102-105).
  * Implemented geometry: head_dim 128, num_q_heads == 4 * num_kv_heads,
- * block_size % 32 == 0.
+ * block_size % 32 == 0 (any positive block_size with prefix_slots).
  */
 int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
 

@@ -74,10 +74,11 @@ constexpr int kMaskBytes = 8 * 64 * 4;                // per stage: each wave's 
 // Tile stages: 8 of one head (HPW 1) or 4 of two heads (HPW 2); the larger is 144 KiB.
 constexpr int kRingBytes = 8 * (2 * kTileBytes + kMaskBytes);
 constexpr int kMaxPages = 512;                        // page numbers of one prefix chunk
+constexpr int kMaxSlotChunk = 2048;                   // prefix keys of one chunk in slot addressing
 constexpr int kMaxTreeSlots = 1024;                   // tree slots cached per work item
-constexpr int kPagesOffset = kRingBytes;
-constexpr int kSlotsOffset = kPagesOffset + kMaxPages * 4;
-constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 153600 of gfx950's 160 KiB
+constexpr int kPagesOffset = kRingBytes;              // page numbers, or the chunk's prefix slots
+constexpr int kSlotsOffset = kPagesOffset + kMaxSlotChunk * 4;
+constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 159744 of gfx950's 160 KiB
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxTileSum = 256.f;                  // per lane half, against the reference
 
@@ -126,6 +127,12 @@ struct AttnParams {
     const int32_t* tables;
     int64_t t_s0;
     const int64_t* tree_slots;
+    // Slot addressing of the prefix (the legacy single-request form, paged_backend.py:20-113):
+    // prefix key k of request r lives at slot pslots[r * ps_s0 + k] instead of its page-table
+    // position.  Null for page-table addressing.
+    const void* pslots;
+    int64_t ps_s0;
+    int32_t ps_i64;
     const uint64_t* anc;
     int32_t words;
     int32_t num_requests;
@@ -218,8 +225,11 @@ __device__ __forceinline__ void order_point() { __builtin_amdgcn_sched_barrier(0
 // its slot (the tile step has a branchy scalar section in its middle).
 __device__ __forceinline__ void pin(float x) { asm volatile("" : : "v"(x)); }
 
-// One work item with HPW KV heads per workgroup.
-template <typename T, int HPW>
+// One work item with HPW KV heads per workgroup.  EXACT keeps every probability to about
+// 2^-17 relative in the P.V product: it is split into a rounded operand-type part and the
+// operand-type rounding of the remainder, and both are multiplied into O (two MFMAs), with
+// the row sums taken in fp32; otherwise the probability is rounded to the operand type once.
+template <typename T, int HPW, bool EXACT>
 __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it) {
     typedef typename Mfma<T>::vec V8;
     typedef typename Mfma<T>::pair V2;
@@ -254,10 +264,13 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const int nt = ntp + (tree_end + kTileKeys - 1) / kTileKeys;
     const int B = p.block_size;
     const int64_t pool_slots = p.num_blocks * B;
+    // Slot addressing is compiled into the EXACT instance only (the legacy entry's mode).
+    const bool slot_mode = EXACT && p.pslots != nullptr;
     const int page0 = it.kbeg / B;
-    const int npages = it.kend > it.kbeg ? (it.kend - 1) / B - page0 + 1 : 0;
+    const int nkeys = it.kend - it.kbeg;
+    const int npages = slot_mode ? 0 : (nkeys > 0 ? (it.kend - 1) / B - page0 + 1 : 0);
     // The planner keeps every item within the LDS page/slot caches and non-empty.
-    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots) {
+    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk)) {
         if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
     }
@@ -267,11 +280,24 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // (at most one page and two slots per thread), so the three lookups cost one round
     // trip, not three.
     static_assert(kMaxPages <= kThreads && kMaxTreeSlots <= 2 * kThreads, "one pass of page and slot loads");
+    static_assert(kMaxSlotChunk <= 4 * kThreads, "one pass of prefix slot loads");
     int32_t* pages = reinterpret_cast<int32_t*>(smem + kPagesOffset);
     int32_t* tslots = reinterpret_cast<int32_t*>(smem + kSlotsOffset);
     int32_t pg = 0;
     int64_t sl[2] = {0, 0};
+    int64_t ps[4] = {0, 0, 0, 0};
     if (tid < npages) pg = p.tables[static_cast<int64_t>(r) * p.t_s0 + page0 + tid];
+    if (slot_mode) {
+        const int64_t base = static_cast<int64_t>(r) * p.ps_s0 + it.kbeg;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < nkeys) {
+                ps[k] = p.ps_i64 ? static_cast<const int64_t*>(p.pslots)[base + i]
+                                 : static_cast<int64_t>(static_cast<const int32_t*>(p.pslots)[base + i]);
+            }
+        }
+    }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         if (tid + k * kThreads < tree_end) sl[k] = p.tree_slots[qbase + tid + k * kThreads];
@@ -294,6 +320,20 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             pg = 0;
         }
         pages[tid] = pg;
+    }
+    if (slot_mode) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = tid + k * kThreads;
+            if (i < nkeys) {
+                int64_t v = ps[k];
+                if (v < 0 || v >= pool_slots) {
+                    set_status(p.status, TV_STATUS_BAD_PAGE);
+                    v = 0;
+                }
+                pages[i] = static_cast<int32_t>(v);
+            }
+        }
     }
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -380,6 +420,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // wave issues at least 2*HPW loads per tile (the count the waits are based on).
     auto fetch = [&](int t) -> int {
         const int tt = t < nt ? t : nt - 1;
+        if (tt < ntp && slot_mode) {
+            const int m0 = kTileKeys * tt;
+            int m = m0 + s_key;
+            if (m >= nkeys) m = m0;
+            return pages[m];
+        }
         if (tt < ntp) {
             const uint32_t tile_pos = static_cast<uint32_t>(it.kbeg + kTileKeys * tt);
             const uint32_t page_abs = pow2 ? (tile_pos >> bshift) : (tile_pos / static_cast<uint32_t>(B));
@@ -395,7 +441,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     uint32_t dmask = 0;        // its ancestor word offset (bytes)
     auto describe = [&](int t, int fetched) {
         const int tt = t < nt ? t : nt - 1;
-        if (tt < ntp) {
+        if (tt < ntp && slot_mode) {
+            const uint32_t slot = static_cast<uint32_t>(fetched);
+            const uint32_t pg = pow2 ? (slot >> bshift) : (slot / static_cast<uint32_t>(B));
+            const uint32_t off = slot - pg * static_cast<uint32_t>(B);
+            dk = k_head_b + static_cast<uint64_t>(pg) * k_page_b + static_cast<uint64_t>(off) * k_key_b + k_chunk_b;
+            dv = v_head_b + static_cast<uint64_t>(pg) * v_page_b + static_cast<uint64_t>(off) * v_key_b + v_chunk_b;
+            dtree = false;
+        } else if (tt < ntp) {
             const uint32_t tile_pos = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(it.kbeg + kTileKeys * tt));
             const uint32_t page_abs = pow2 ? (tile_pos >> bshift) : (tile_pos / static_cast<uint32_t>(B));
             const uint32_t off0 = tile_pos - page_abs * static_cast<uint32_t>(B);
@@ -510,18 +563,25 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     };
     // Probabilities of tile scores `s` against the current reference, packed as the
     // P^T operand, and this lane's sum of the packed values.
-    auto probabilities = [&](const f32x16& s, V8 (&pb)[2]) -> float {
+    auto probabilities = [&](const f32x16& s, V8 (&pb)[2], V8 (&pl)[2]) -> float {
         float l0 = 0.f, l1 = 0.f;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
             for (int t8 = 0; t8 < 8; ++t8) {
-                pb[kk][t8] = static_cast<T>(__builtin_amdgcn_exp2f(fmaf(s[8 * kk + t8], cs, nmc)));
+                const float pr = __builtin_amdgcn_exp2f(fmaf(s[8 * kk + t8], cs, nmc));
+                pb[kk][t8] = static_cast<T>(pr);
+                if constexpr (EXACT) {
+                    pl[kk][t8] = static_cast<T>(pr - static_cast<float>(pb[kk][t8]));
+                    if (t8 & 1) l1 += pr; else l0 += pr;
+                }
             }
+            if constexpr (!EXACT) {
 #pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                const V2 two = {pb[kk][2 * q2], pb[kk][2 * q2 + 1]};
-                if (q2 & 1) l1 = Mfma<T>::dot2(two, l1); else l0 = Mfma<T>::dot2(two, l0);
+                for (int q2 = 0; q2 < 4; ++q2) {
+                    const V2 two = {pb[kk][2 * q2], pb[kk][2 * q2 + 1]};
+                    if (q2 & 1) l1 = Mfma<T>::dot2(two, l1); else l0 = Mfma<T>::dot2(two, l0);
+                }
             }
         }
         return l0 + l1;
@@ -534,7 +594,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // sums) fills the slots.  No MFMA of the step waits for a VALU result of the same
     // step, so the matrix core and the VALU work at once.  piece(slot) adds the DMA
     // issue of a later tile, a step at a time.
-    auto step = [&](const f32x16& s, f32x16& sn, const V8 (&pb_prev)[2], V8 (&pb)[2], const int kst,
+    auto step = [&](const f32x16& s, f32x16& sn, const V8 (&pb_prev)[2], V8 (&pb)[2], const V8 (&pl_prev)[2],
+                    V8 (&pl)[2], const int kst,
                     const int vst, auto&& piece) -> float {
         V8 ka[8];
         i16x4 vlo[8], vhi[8];
@@ -559,6 +620,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 const int j = sl >> 1, kk = j >> 2, db = j & 3;
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(vlo[j], vhi[j], 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
+                if constexpr (EXACT) acc[db] = Mfma<T>::run(a, pl_prev[kk], acc[db]);
             }
         };
         auto slot_read = [&](int sl) {
@@ -571,8 +633,17 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         auto pack = [&](int q) {  // probabilities 2q, 2q+1
             pb[q >> 2][2 * (q & 3)] = static_cast<T>(pr[2 * q]);
             pb[q >> 2][2 * (q & 3) + 1] = static_cast<T>(pr[2 * q + 1]);
+            if constexpr (EXACT) {
+                pl[q >> 2][2 * (q & 3)] = static_cast<T>(pr[2 * q] - static_cast<float>(pb[q >> 2][2 * (q & 3)]));
+                pl[q >> 2][2 * (q & 3) + 1] =
+                    static_cast<T>(pr[2 * q + 1] - static_cast<float>(pb[q >> 2][2 * (q & 3) + 1]));
+            }
         };
         auto rsum = [&](int q) {
+            if constexpr (EXACT) {
+                if (q & 1) l1 += pr[2 * q] + pr[2 * q + 1]; else l0 += pr[2 * q] + pr[2 * q + 1];
+                return;
+            }
             const V2 two = {pb[q >> 2][2 * (q & 3)], pb[q >> 2][2 * (q & 3) + 1]};
             if (q & 1) {
                 l1 = Mfma<T>::dot2(two, l1);
@@ -632,7 +703,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // offset; a new page is read from the LDS page list, prefetched one page ahead,
     // when the current one is used up.  Pages hold whole tiles when B is a multiple
     // of the tile (the item's first key is).
-    const int t_fast = (B % kTileKeys == 0) ? max(0, nfull - (NS - 2)) : 0;
+    const int t_fast = (B % kTileKeys == 0 && !slot_mode && !EXACT) ? max(0, nfull - (NS - 2)) : 0;
     uint64_t fk = 0, fv = 0;     // K and V base of the next streamed tile (head h0)
     int f_left = 0, f_pidx = 0;  // tiles left in its page; the page's index in `pages`
     int32_t f_next = 0;          // page number at f_pidx + 1
@@ -678,9 +749,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     wait_vmcnt<(NS - 3) * LPT>();
     __syncthreads();
     f32x16 s = f32x16{};
-    V8 pb_prev[2];
+    V8 pb_prev[2], pl_prev[2];
     pb_prev[0] = V8{};
     pb_prev[1] = V8{};
+    pl_prev[0] = V8{};
+    pl_prev[1] = V8{};
     if (wave_active) {
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
@@ -692,7 +765,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     }
     // Fast steps.  Active waves alternate two register sets for the scores and the
     // probabilities by tile parity (NS is even, so the parity of t is that of b), so no
-    // copies between steps; inactive waves only stage their share of the tiles.
+    // copies between steps; inactive waves only stage their share of the tiles.  (EXACT
+    // items run every step in the general loop.)
+    if constexpr (!EXACT) {
     if (wave_active) {
         f32x16 sc[2];
         V8 pp[2][2];
@@ -718,12 +793,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     if (sl == 12) fast_advance();
                 };
                 f32x16& s_cur = sc[b & 1];
-                float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], ((b + 1) % NS) * TILE_SET,
-                                ((b + NS - 1) % NS) * TILE_SET, piece);
+                float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1],
+                                ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET, piece);
                 const bool need = !(lt <= kMaxTileSum);
                 if (__any(need)) {
                     raise_max(s_cur, need);
-                    lt = probabilities(s_cur, pp[(b + 1) & 1]);
+                    lt = probabilities(s_cur, pp[(b + 1) & 1], pp[(b + 1) & 1]);
                 }
                 l_run += lt;
             }
@@ -748,6 +823,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 fast_advance();
             }
         }
+    }
     }
     // The remaining steps: masks, partial and tree tiles, general DMA.
     int pf = fetch(t_fast + NS - 2);
@@ -776,16 +852,21 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             if (wave_active) {
                 if (t >= nfull && t > 0) mask_tile(s, b, t);
                 f32x16 sn;
-                V8 pb[2];
-                float lt = step(s, sn, pb_prev, pb, ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET, piece);
+                V8 pb[2], pl[2];
+                float lt = step(s, sn, pb_prev, pb, pl_prev, pl, ((b + 1) % NS) * TILE_SET,
+                                ((b + NS - 1) % NS) * TILE_SET, piece);
                 const bool need = !(lt <= kMaxTileSum);
                 if (__any(need)) {
                     raise_max(s, need);
-                    lt = probabilities(s, pb);
+                    lt = probabilities(s, pb, pl);
                 }
                 l_run += lt;
                 pb_prev[0] = pb[0];
                 pb_prev[1] = pb[1];
+                if constexpr (EXACT) {
+                    pl_prev[0] = pl[0];
+                    pl_prev[1] = pl[1];
+                }
                 s = sn;
             } else {
 #pragma unroll
@@ -806,6 +887,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * kRowBytes));
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
+                if constexpr (EXACT) acc[db] = Mfma<T>::run(a, pl_prev[kk], acc[db]);
             }
         }
     }
@@ -841,7 +923,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     }
 }
 
-template <typename T>
+template <typename T, bool EXACT>
 __global__ void __launch_bounds__(kThreads)
 tree_attention_kernel(const AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
@@ -858,8 +940,8 @@ tree_attention_kernel(const AttnParams p) {
         return;
     }
     switch (it.hpw) {
-        case 1: run_item<T, 1>(p, smem, it); break;
-        case 2: run_item<T, 2>(p, smem, it); break;
+        case 1: run_item<T, 1, EXACT>(p, smem, it); break;
+        case 2: run_item<T, 2, EXACT>(p, smem, it); break;
         default:
             if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
             break;
@@ -1006,8 +1088,14 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: %d query heads over %d KV heads (implemented: 4 per KV head)",
                     a->num_q_heads, a->num_kv_heads);
     }
-    if (a->block_size < 32 || a->block_size % 32) {
+    if (a->prefix_slots ? a->block_size < 1 : (a->block_size < 32 || a->block_size % 32)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: block_size %d is not a multiple of 32", a->block_size);
+    }
+    if (a->prefix_slots && a->prefix_slots_stride < 0) {
+        return fail(TV_ERR_INVALID, "tree_attention: negative prefix slot stride");
+    }
+    if (a->prefix_slots && !a->exact_probabilities) {
+        return fail(TV_ERR_UNSUPPORTED, "tree_attention: slot-addressed prefixes run with exact probabilities");
     }
     // The online softmax orders scores by their value times the scale.
     if (!(a->scale > 0.f) || !isfinite(a->scale)) {
@@ -1091,6 +1179,9 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     p.tables = a->block_tables;
     p.t_s0 = a->block_table_stride;
     p.tree_slots = a->tree_slots;
+    p.pslots = a->prefix_slots;
+    p.ps_s0 = a->prefix_slots_stride;
+    p.ps_i64 = a->prefix_slots_is_int64 != 0;
     p.anc = a->ancestor_words;
     p.words = a->ancestor_words_per_row;
     p.num_requests = a->num_requests;
@@ -1104,13 +1195,22 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     p.ws_ml = a->workspace ? reinterpret_cast<float2*>(static_cast<char*>(a->workspace) + o_span) : nullptr;
     p.status = a->status;
     hipStream_t s = as_stream(stream);
+    const bool exact = a->exact_probabilities != 0;
     if (a->in_dtype == TV_BF16) {
-        hipLaunchKernelGGL(tree_attention_kernel<__bf16>, dim3(a->num_items), dim3(kThreads), 0, s, p);
+        if (exact) {
+            hipLaunchKernelGGL((tree_attention_kernel<__bf16, true>), dim3(a->num_items), dim3(kThreads), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((tree_attention_kernel<__bf16, false>), dim3(a->num_items), dim3(kThreads), 0, s, p);
+        }
         if (a->num_groups > 0) {
             hipLaunchKernelGGL(merge_partials_kernel<__bf16>, dim3(a->num_groups, kRowsPerItem / 8), dim3(256), 0, s, p);
         }
     } else {
-        hipLaunchKernelGGL(tree_attention_kernel<_Float16>, dim3(a->num_items), dim3(kThreads), 0, s, p);
+        if (exact) {
+            hipLaunchKernelGGL((tree_attention_kernel<_Float16, true>), dim3(a->num_items), dim3(kThreads), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((tree_attention_kernel<_Float16, false>), dim3(a->num_items), dim3(kThreads), 0, s, p);
+        }
         if (a->num_groups > 0) {
             hipLaunchKernelGGL(merge_partials_kernel<_Float16>, dim3(a->num_groups, kRowsPerItem / 8), dim3(256), 0, s, p);
         }

@@ -29,6 +29,7 @@ constexpr int kRowsPerItem = 256;   // score rows of one workgroup
 constexpr int kHeadDim = 128;
 constexpr int kMinChunkKeys = 64;   // shortest prefix chunk worth a partial result
 constexpr int kMaxChunkPages = 512; // page numbers a workgroup caches in LDS
+constexpr int kMaxSlotChunk = 2048; // prefix slots a workgroup caches in LDS (slot addressing)
 constexpr int kMaxTreeNodes = 1024; // tree slots a workgroup caches in LDS
 constexpr int64_t kFillRounds = 4;  // item rounds the chunk target is refitted for
 
@@ -145,22 +146,13 @@ void place_for_xcds(std::vector<Item>& items) {
     }
 }
 
-}  // namespace
-}  // namespace tv
-
-using namespace tv;
-
-extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
-                                      int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
-                                      int32_t num_compute_units, int32_t chunk_keys, int32_t* items_host,
-                                      int32_t* groups_host, tv_attention_plan_info* info) {
-    clear_error();
+// The plan for chunks of at most max_chunk keys (a multiple of 32).
+int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32_t num_requests,
+         int32_t num_kv_heads, int32_t num_compute_units, int32_t chunk_keys, int64_t max_chunk,
+         int32_t* items_host, int32_t* groups_host, tv_attention_plan_info* info) {
     if (!info || !prefix_lens_host || !node_counts_host) return fail(TV_ERR_INVALID, "plan: null argument");
     if (num_requests < 1) return fail(TV_ERR_INVALID, "plan: at least one request is required");
     if (num_kv_heads < 1) return fail(TV_ERR_INVALID, "plan: num_kv_heads must be positive");
-    if (block_size < 32 || block_size % 32) {
-        return fail(TV_ERR_UNSUPPORTED, "plan: block_size %d is not a positive multiple of 32", block_size);
-    }
     if (num_compute_units < 1) return fail(TV_ERR_INVALID, "plan: num_compute_units must be positive");
     if (chunk_keys < 0 || chunk_keys % 32) {
         return fail(TV_ERR_INVALID, "plan: chunk_keys %d must be a non-negative multiple of 32", chunk_keys);
@@ -183,8 +175,6 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
         total_cost += groups * blocks * cost_weight(hpw) * (static_cast<int64_t>(p) + t);
     }
     const int64_t target = std::max<int64_t>(kMinChunkKeys, total_cost / num_compute_units);
-    // Longest chunk whose pages fit the LDS page cache wherever it starts.
-    const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
     if (chunk_keys > max_chunk) {
         return fail(TV_ERR_INVALID, "plan: chunk_keys %d exceeds %lld", chunk_keys, (long long)max_chunk);
     }
@@ -302,4 +292,32 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
     const int64_t ml_bytes = static_cast<int64_t>(num_slots) * kRowsPerItem * 8;
     info->workspace_bytes = num_slots ? round_up(o_bytes, 256) + round_up(ml_bytes, 256) : 0;
     return TV_OK;
+}
+
+}  // namespace
+}  // namespace tv
+
+using namespace tv;
+
+extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
+                                      int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                      int32_t num_compute_units, int32_t chunk_keys, int32_t* items_host,
+                                      int32_t* groups_host, tv_attention_plan_info* info) {
+    clear_error();
+    if (block_size < 32 || block_size % 32) {
+        return fail(TV_ERR_UNSUPPORTED, "plan: block_size %d is not a positive multiple of 32", block_size);
+    }
+    // Longest chunk whose pages fit the LDS page cache wherever it starts.
+    const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
+    return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, num_compute_units, chunk_keys,
+                max_chunk, items_host, groups_host, info);
+}
+
+extern "C" int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
+                                            int32_t num_requests, int32_t num_kv_heads, int32_t num_compute_units,
+                                            int32_t chunk_keys, int32_t* items_host, int32_t* groups_host,
+                                            tv_attention_plan_info* info) {
+    clear_error();
+    return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, num_compute_units, chunk_keys,
+                kMaxSlotChunk, items_host, groups_host, info);
 }

@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "tv_commit_slots",
     "tv_truncate_accepted",
     "tv_tree_attention_plan",
+    "tv_tree_attention_plan_slots",
     "tv_pack_ancestor_words",
     "tv_tree_attention",
     "tv_sizeof_rope_scatter_args",
@@ -107,6 +108,10 @@ class TreeAttentionArgs(ctypes.Structure):
         ("workspace_bytes", c_int64),
         ("status", c_void_p),
         ("device_counts", c_void_p),
+        ("prefix_slots", c_void_p),
+        ("prefix_slots_stride", c_int64),
+        ("prefix_slots_is_int64", c_int32),
+        ("exact_probabilities", c_int32),
     ]
 
 
@@ -160,6 +165,9 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_tree_attention_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32, c_int32,
                                            c_int32, c_int32, POINTER(c_int32), POINTER(c_int32),
                                            POINTER(PlanInfo)]
+    lib.tv_tree_attention_plan_slots.restype = c_int32
+    lib.tv_tree_attention_plan_slots.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32, c_int32,
+                                                 c_int32, POINTER(c_int32), POINTER(c_int32), POINTER(PlanInfo)]
     lib.tv_pack_ancestor_words.restype = c_int32
     lib.tv_pack_ancestor_words.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                            c_int32, c_void_p, c_void_p, c_void_p]

@@ -4,9 +4,12 @@ Every public entry keeps the reference's signature, argument meaning and ValueEr
 conditions, and runs ONE hand-written HIP kernel (libtreeverify: tv_tree_attention).
 The reference's numerical variants (frozen FP32 ``reference``, ``prefix``, grouped
 ``gqa``) differ only in tiling and precision knobs; here they are one kernel with
-bf16/f16 MFMA products, fp32 accumulation and online softmax, and probabilities
-rounded to the operand type for the P.V product (as the reference's gqa backend,
-tree_gqa.py:102-105).
+bf16/f16 MFMA products, fp32 accumulation and online softmax, in two probability
+modes: ``auto`` and ``gqa`` round each probability to the operand type for the P.V
+product (as the reference's gqa backend, tree_gqa.py:102-105); the explicit FP32
+entries (``reference``, ``prefix``, and their modules' other entries) keep it to about
+2^-17 relative (two MFMAs: its rounding and the rounding of the remainder) and sum it
+in fp32, the reference's "never BF16 probabilities" (paged_backend.py:248-256).
 
 Two launch modes, chosen per call:
 
@@ -242,7 +245,7 @@ def _capture_id(stream: int) -> int:
 
 
 def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int, chunk_keys: int,
-                     stream: int) -> torch.Tensor:
+                     stream: int, exact: bool) -> torch.Tensor:
     """Graph-capturable launch that follows the live device metadata on every replay."""
     from .target_graph import GraphedTreeAttention
 
@@ -255,16 +258,19 @@ def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int,
     if graphed.prepared_capture != capture:
         graphed.prepare(metadata)   # recorded once at the head of this graph's sequence
         graphed.prepared_capture = capture
-    return graphed(q, k_pool, v_pool, metadata, scale, out, prepared=True)
+    return graphed(q, k_pool, v_pool, metadata, scale, out, prepared=True, exact=exact)
 
 
-def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> torch.Tensor:
+def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0, exact: bool = False) -> torch.Tensor:
+    """Enqueue the attention of `metadata` into `out`.  exact=True keeps every probability
+    to ~2^-17 relative in the P.V product (the reference's FP32 entries); otherwise it is
+    rounded to the operand type once (the reference's grouped bf16-P kernel)."""
     if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
         q = q.contiguous()
     num_kv_heads = int(k_pool.shape[2])
     stream = torch.cuda.current_stream(q.device).cuda_stream
     if torch.cuda.is_current_stream_capturing():
-        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, chunk_keys, stream)
+        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, chunk_keys, stream, exact)
     per_meta = _derived.get(id(metadata))
     if per_meta is None:
         per_meta = _per_metadata(metadata)
@@ -280,13 +286,15 @@ def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0) -> 
     a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
     a.out_dtype = _device.dtype_code(out.dtype)
     a.scale = scale
+    a.exact_probabilities = 1 if exact else 0
     _lib.check(_lib.library().tv_tree_attention(ctypes.byref(a), stream), "tree_attention")
     return out
 
 
-def _launch_new(q, k_pool, v_pool, metadata, scale, dtype) -> torch.Tensor:
+def _launch_new(q, k_pool, v_pool, metadata, scale, dtype, *, exact: bool) -> torch.Tensor:
     """Launch into a new output of `dtype` (the checked entries' allocation, tree_attention.py:36)."""
-    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device))
+    return _launch(q, k_pool, v_pool, metadata, scale, torch.empty(q.shape, dtype=dtype, device=q.device),
+                   exact=exact)
 
 
 def packed_tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor, metadata, scale: float,
@@ -323,13 +331,130 @@ def packed_tree_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.T
 def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_k, qq_bias, scale,
                          num_queries_per_kv, block_size, logical_kv_slots=None, logical_kv_starts=None,
                          logical_kv_lens=None):
-    """Legacy single-request entry (paged_backend.py:309-415).
+    """Legacy single-request entry (paged_backend.py:309-415), as the legacy c1 path calls it
+    (models/qwen3.py:270-302): one request whose keys are named by a logical slot vector,
+    ``logical_kv_slots[0, pos]`` for pos < seq_len (the committed prefix, then the T tree
+    nodes), over a pool viewed as ``block_size``-token pages (16 in the c1 path), and a
+    request-local ``qq_bias[T, T]`` of 0 / -inf.  A key at position pos is visible to tree
+    row i iff pos <= P + i and, for a tree key, its bias is 0 (paged_backend.py:82-91).
 
-    Multi-request calls are rejected exactly as in the reference.  The legacy
-    logical-slot addressing (a history-sized slot vector instead of page tables)
-    is not implemented by this build: callers use PackedTreeMetadata.
+    Runs the HIP kernel in slot-addressed mode with FP32 probabilities (the legacy kernel
+    is the frozen FP32 one, paged_backend.py:20-113).  Like the reference, it reads the
+    sequence length from the device (one synchronisation).  Multi-request calls are
+    rejected exactly as in the reference; the block-table form without logical slots or
+    bias runs the external jetspec kernel in the reference (paged_backend.py:362-363),
+    which is not part of this build, and is rejected too.
     """
-    if int(seq_lens_k.shape[0]) != 1:
+    num_seqs = int(seq_lens_k.shape[0])
+    if num_seqs != 1:
         raise ValueError("multi-request tree verification requires explicit PackedTreeMetadata")
-    raise ValueError("legacy logical-slot tree attention is not part of the MI355X build; "
-                     "build PackedTreeMetadata and call packed_tree_attention")
+    if logical_kv_slots is None or qq_bias is None:
+        raise ValueError("block-table tree attention (the external jetspec kernel) is not part of the MI355X "
+                         "build; pass logical_kv_slots and qq_bias, or build PackedTreeMetadata")
+    if q.ndim != 3 or k_pool.ndim != 4 or k_pool.shape != v_pool.shape:
+        raise ValueError("unsupported packed query/KV head geometry")
+    total_q, num_query_heads, head_size = q.shape
+    device = _device.require_gpu(q, k_pool, v_pool, logical_kv_slots, qq_bias, seq_lens_k,
+                                 what="paged_tree_attention")
+    if (q.stride(-1) != 1 or k_pool.shape[3] != head_size or int(k_pool.shape[1]) != int(block_size)
+            or isinstance(num_queries_per_kv, bool) or num_query_heads != k_pool.shape[2] * num_queries_per_kv):
+        raise ValueError("unsupported packed query/KV head geometry")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k_pool.dtype != q.dtype or v_pool.dtype != q.dtype:
+        raise ValueError("the MI355X tree-attention kernel takes bf16 or f16 operands (FP32 Q/K/V unsupported)")
+    if num_queries_per_kv != 4 or head_size != 128:
+        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 4 query heads per KV head")
+    if logical_kv_slots.dtype not in (torch.int32, torch.int64):
+        raise ValueError("logical KV slots must be int32 or int64")
+    if qq_bias.ndim != 2 or qq_bias.shape[0] < total_q or qq_bias.shape[1] < total_q:
+        raise ValueError("qq_bias must be a [tree nodes, tree nodes] matrix")
+    seq_len = int(seq_lens_k[0].item())
+    prefix = seq_len - total_q
+    slots = logical_kv_slots.reshape(-1)
+    if prefix < 0 or slots.numel() < seq_len or total_q < 1:
+        raise ValueError("logical KV slots must cover the prefix and every tree node")
+    if total_q > 1024:
+        raise ValueError("the MI355X tree-attention kernel takes at most 1024 tree nodes per request")
+    if not slots.is_contiguous():
+        slots = slots.contiguous()
+    bias = torch.as_strided(qq_bias, (total_q, total_q), (qq_bias.stride(0), qq_bias.stride(1))).to(
+        torch.float32).contiguous().view(-1)
+    # The kernel reads the tree visibility as bits: a bias other than 0 / -inf (which the
+    # reference would add to the score) cannot be represented and is refused.
+    if not bool(((bias == 0) | (bias == float("-inf"))).all()):
+        raise ValueError("qq_bias entries must be 0 (visible) or -inf (hidden)")
+    num_kv_heads = int(k_pool.shape[2])
+    lib = _lib.library()
+    i32 = dict(dtype=torch.int32, device=device)
+    cu = torch.tensor([0, total_q], **i32)
+    counts = torch.tensor([total_q], **i32)
+    rows_local = torch.arange(total_q, **i32)
+    requests = torch.zeros(total_q, **i32)
+    bias_offsets = torch.tensor([0, total_q * total_q], dtype=torch.int64, device=device)
+    tree_slots = slots[prefix:prefix + total_q].to(torch.int64)
+    prefix_lens = torch.tensor([prefix], **i32)
+    table = torch.full((1, 1), -1, **i32)
+    stream = _device.stream_handle(device)
+    status = _device.status_word(device)
+    per_row = (total_q + 63) // 64
+    words = torch.empty((total_q, per_row), dtype=torch.int64, device=device)
+    _lib.check(lib.tv_pack_ancestor_words(bias.data_ptr(), bias_offsets.data_ptr(), requests.data_ptr(),
+                                          rows_local.data_ptr(), counts.data_ptr(), total_q, 1, per_row,
+                                          words.data_ptr(), status.data_ptr(), stream), "pack_ancestor_words")
+    info = _lib.PlanInfo()
+    prefixes_host = (ctypes.c_int32 * 1)(prefix)
+    nodes_host = (ctypes.c_int32 * 1)(total_q)
+    cus = _device.compute_units(device.index if device.index is not None else torch.cuda.current_device())
+    _lib.check(lib.tv_tree_attention_plan_slots(prefixes_host, nodes_host, 1, num_kv_heads, cus, 0, None, None,
+                                                ctypes.byref(info)), "tree_attention_plan_slots")
+    items = np.zeros((max(info.num_items, 1), 8), dtype=np.int32)
+    groups = np.zeros((max(info.num_groups, 1), 8), dtype=np.int32)
+    _lib.check(lib.tv_tree_attention_plan_slots(
+        prefixes_host, nodes_host, 1, num_kv_heads, cus, 0, items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+        groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(info)), "tree_attention_plan_slots")
+    items_dev = torch.from_numpy(items).to(device)
+    groups_dev = torch.from_numpy(groups).to(device)
+    workspace = torch.empty(max(int(info.workspace_bytes), 1), dtype=torch.uint8, device=device)
+    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    out = torch.empty_like(q)
+    a = _lib.TreeAttentionArgs()
+    a.q = q.data_ptr()
+    a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
+    a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
+    for i in range(4):
+        a.k_stride[i] = k_pool.stride(i)
+        a.v_stride[i] = v_pool.stride(i)
+    a.num_blocks = int(k_pool.shape[0])
+    a.in_dtype = _device.dtype_code(q.dtype)
+    a.out = out.data_ptr()
+    a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
+    a.out_dtype = _device.dtype_code(out.dtype)
+    a.cu_seqlens_q = cu.data_ptr()
+    a.prefix_lens = prefix_lens.data_ptr()
+    a.node_counts = counts.data_ptr()
+    a.block_tables = table.data_ptr()
+    a.block_table_stride = 1
+    a.tree_slots = tree_slots.data_ptr()
+    a.ancestor_words = words.data_ptr()
+    a.ancestor_words_per_row = per_row
+    a.num_requests = 1
+    a.total_queries = total_q
+    a.num_q_heads = num_query_heads
+    a.num_kv_heads = num_kv_heads
+    a.head_dim = head_size
+    a.block_size = int(block_size)
+    a.scale = float(scale)
+    a.items = items_dev.data_ptr()
+    a.num_items = info.num_items
+    a.groups = groups_dev.data_ptr() if info.num_groups else None
+    a.num_groups = info.num_groups
+    a.num_partial_slots = info.num_partial_slots
+    a.workspace = workspace.data_ptr() if info.workspace_bytes else None
+    a.workspace_bytes = int(info.workspace_bytes)
+    a.status = status.data_ptr()
+    a.prefix_slots = slots.data_ptr()
+    a.prefix_slots_stride = 0
+    a.prefix_slots_is_int64 = 1 if slots.dtype == torch.int64 else 0
+    a.exact_probabilities = 1
+    _lib.check(lib.tv_tree_attention(ctypes.byref(a), stream), "tree_attention (slot addressed)")
+    return out

@@ -2,10 +2,11 @@
 
 The qualification harness resolves candidates as ``module:function`` and requires an
 ``output_dtype`` keyword (benchmarks/jetspec_tree_kernel_qualification.py:33-55); these
-entries keep the reference's names, keywords and ValueError messages.  Their tiling
-knobs (query tile, warps, register cap) are CUDA/Triton launch parameters that do not
-exist on this kernel: they are validated as the reference validates them and then
-fixed by the kernel.
+entries keep the reference's names, keywords and ValueError messages, and its numerics
+contract: FP32 probabilities (the kernel's exact-probability mode), never bf16 ones
+(tree_attention.py:1-10).  Their tiling knobs (query tile, warps, register cap) are
+CUDA/Triton launch parameters that do not exist on this kernel: they are validated as
+the reference validates them and then fixed by the kernel.
 """
 from __future__ import annotations
 
@@ -16,7 +17,7 @@ def packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_quer
                                     output_dtype=None):
     """tree_attention.py:40-62 (explicit FP32 output supported)."""
     dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
-    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype)
+    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype, exact=True)
 
 
 def packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *, output_dtype=None,
@@ -27,7 +28,7 @@ def packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_pe
     if isinstance(num_warps, bool) or num_warps not in (4, 8, 16):
         raise ValueError("num_warps must be 4, 8 or 16")
     dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
-    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype)
+    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype, exact=True)
 
 
 def packed_tree_attention_register_tuned(q, k_pool, v_pool, metadata, scale, num_queries_per_kv, *,

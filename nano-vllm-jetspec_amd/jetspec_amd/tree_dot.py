@@ -1,4 +1,5 @@
-"""Entry of speculative/jetspec/tree_dot.py (the reference's matrix-core precision experiment)."""
+"""Entry of speculative/jetspec/tree_dot.py (the reference's matrix-core precision experiment,
+TF32x3 products with FP32 probabilities): the kernel's exact-probability mode."""
 from __future__ import annotations
 
 from .paged_backend import _launch_new, _validate
@@ -17,4 +18,4 @@ def packed_tree_attention_dot(q, k_pool, v_pool, metadata, scale, num_queries_pe
         return packed_tree_attention_reference(q, k_pool, v_pool, metadata, scale, num_queries_per_kv,
                                                output_dtype=output_dtype)
     dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
-    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype)
+    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype, exact=True)

@@ -2,8 +2,9 @@
 
 ``packed_tree_attention(..., backend="gqa")`` dispatches here, as paged_backend.py:273-276
 does.  The kernel's own design already is KV-head-centric with bf16 probabilities in the
-P.V product (tree_gqa.py:102-105); the reference's ablation switches are validated and
-fixed.
+P.V product (tree_gqa.py:102-105); ``fp32_probability=True`` selects the kernel's exact
+probability mode (the reference's FP32_P switch), and the tiling switches are validated
+and fixed.
 """
 from __future__ import annotations
 
@@ -22,4 +23,4 @@ def packed_tree_attention_gqa(q, k_pool, v_pool, metadata, scale, num_queries_pe
     if num_queries_per_kv not in (1, 2, 4, 8, 16):
         raise ValueError("grouped tree attention requires power-of-two GQA <=16")
     dtype = _validate(q, k_pool, v_pool, metadata, num_queries_per_kv, output_dtype)
-    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype)
+    return _launch_new(q, k_pool, v_pool, metadata, scale, dtype, exact=bool(fp32_probability))

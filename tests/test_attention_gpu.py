@@ -142,9 +142,11 @@ def test_fp32_output_round_trips_to_bf16_output_and_repeat_is_bitwise():
     assert out32.dtype == torch.float32
     assert bits_equal(out32.to(torch.bfloat16), out)
     assert bits_equal(out, again)
+    # The launch-only prefix entry keeps FP32 probabilities, like the reference's
+    # split-exact kernel: it equals the explicit FP32 backend, not the bf16-P auto path.
     pre = torch.empty_like(q)
     packed_tree_attention_prefix_prevalidated(q, k, v, meta, 128 ** -0.5, 4, pre)
-    assert bits_equal(pre, out)
+    assert bits_equal(pre, packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4, backend="reference"))
 
 
 def test_other_requests_cannot_affect_neighbors():

@@ -83,3 +83,15 @@ def test_grouped_entry_requires_half_precision_before_geometry():
     q = q.to(torch.bfloat16)
     with pytest.raises(ValueError, match="power-of-two GQA <=16"):
         packed_tree_attention_gqa(q, q, q, None, 1.0, 3)
+
+
+def test_legacy_entry_rejections_before_any_device_work():
+    """paged_backend.py:323-325: more than one sequence is refused; the block-table form (no
+    logical slots or no bias) runs the external jetspec kernel, which this build lacks."""
+    from jetspec_amd import paged_tree_attention
+
+    q, k, v = _cpu_operands()
+    with pytest.raises(ValueError, match="multi-request tree verification requires explicit PackedTreeMetadata"):
+        paged_tree_attention(q, k, v, None, None, torch.zeros(2), None, 1.0, 4, 256)
+    with pytest.raises(ValueError, match="external jetspec kernel"):
+        paged_tree_attention(q, k, v, None, None, torch.zeros(1), None, 1.0, 4, 256)
