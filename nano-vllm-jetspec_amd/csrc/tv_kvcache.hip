@@ -71,7 +71,7 @@ store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
 //                      every row into the workspace, synchronises, and scatters
 //                      them (the reference's order; never taken by the served
 //                      callers); an invalid slot -> nothing is written.
-// Up to kFusedMaxSlots slots (every served round) take one launch instead,
+// Up to kFusedMaxSlots slots (typical served rounds) take one launch instead,
 // commit_fused_kernel, which does the same per row without the flag pass.
 
 constexpr int kCheckThreads = 256;
@@ -183,6 +183,15 @@ template <typename Unit>
 __global__ void __launch_bounds__(kMoveThreads)
 commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
                    const int32_t* __restrict__ flags, int32_t num_flags, Unit* __restrict__ staging) {
+    // This workgroup's row slots are loaded together with the flag words (one round trip
+    // before the copy, not two).
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kMoveRows;
+    const int32_t nrows = static_cast<int32_t>(g.n - i0 < kMoveRows ? g.n - i0 : kMoveRows);
+    int64_t my_src = 0, my_dst = 0;
+    if (threadIdx.x < nrows) {
+        my_src = src[i0 + threadIdx.x];
+        my_dst = dst[i0 + threadIdx.x];
+    }
     const int32_t f = read_flags(flags, num_flags);
     if (f & kFlagInvalid) return;
     const int32_t upr = g.units_per_row;
@@ -205,12 +214,10 @@ commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* _
         return;
     }
     __shared__ int64_t row_src[kMoveRows], row_dst[kMoveRows];
-    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * kMoveRows;
-    const int32_t nrows = static_cast<int32_t>(g.n - i0 < kMoveRows ? g.n - i0 : kMoveRows);
     const int32_t plane = blockIdx.y;
     if (threadIdx.x < nrows) {
-        row_src[threadIdx.x] = slot_offset(g, src[i0 + threadIdx.x]);
-        row_dst[threadIdx.x] = slot_offset(g, dst[i0 + threadIdx.x]);
+        row_src[threadIdx.x] = slot_offset(g, my_src);
+        row_dst[threadIdx.x] = slot_offset(g, my_dst);
     }
     __syncthreads();
     copy_rows<Unit>(g, plane, row_src, row_dst, nrows, 0u);
@@ -223,8 +230,38 @@ commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* _
 // the clean rows among rows 8(x-1)..8(x-1)+7 of plane y; workgroup (0, 0) finds the
 // dirty rows and moves them through the workspace (gather all, barrier, scatter
 // all), the reference's order.  Every workgroup validates every slot first, so an
-// invalid map writes nothing anywhere.
-constexpr int64_t kFusedMaxSlots = 2048;
+// invalid map writes nothing anywhere.  Each copy workgroup tests its 8 rows against
+// every slot (8n compares, its share of the n slots loaded once), so the one-launch form
+// is kept to n <= 512, where that costs less than a second launch; larger batches take
+// commit_check + commit_move.
+constexpr int64_t kFusedMaxSlots = 512;
+constexpr int kFusedHash = 2 * kFusedMaxSlots;   // open-addressing slots per hash set (load <= 1/2)
+
+// Open-addressing set of non-negative 32-bit slots in LDS (empty entries are -1),
+// for the dirty-row test in O(n): insert every slot of one list, then probe.
+__device__ __forceinline__ uint32_t slot_hash(int32_t v) {
+    return (static_cast<uint32_t>(v) * 2654435761u) >> (32 - 10);   // 10 bits: kFusedHash entries
+}
+static_assert(kFusedHash == 1024, "slot_hash takes 10 bits");
+
+__device__ __forceinline__ void hash_insert(int32_t* table, int32_t v) {
+    uint32_t h = slot_hash(v);
+    while (true) {
+        const int32_t prev = atomicCAS(&table[h], -1, v);
+        if (prev == -1 || prev == v) return;
+        h = (h + 1) & (kFusedHash - 1);
+    }
+}
+
+__device__ __forceinline__ bool hash_contains(const int32_t* table, int32_t v) {
+    uint32_t h = slot_hash(v);
+    while (true) {
+        const int32_t e = table[h];
+        if (e == v) return true;
+        if (e == -1) return false;
+        h = (h + 1) & (kFusedHash - 1);
+    }
+}
 
 template <typename Unit>
 __global__ void __launch_bounds__(kMoveThreads)
@@ -233,19 +270,22 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
     if (blockIdx.x == 0 && blockIdx.y != 0) return;
     const int32_t n = static_cast<int32_t>(g.n);
     if (blockIdx.x == 0) {
-        // The dirty-row mover, the launch's longest workgroup: its all-pairs test
-        // decides when the kernel ends even when no row is dirty.  The slot lists go to
-        // LDS as 32-bit values (the host takes this path only for pools of fewer than
-        // 2^31 slots), padded to a multiple of 4 with -1, which equals no valid slot,
-        // and each row is tested against four slots of each list per 128-bit broadcast
-        // read.  18 KB of LDS per workgroup still lets a CU hold 8 of them.
-        __shared__ __attribute__((aligned(16))) int32_t s_src[kFusedMaxSlots], s_dst[kFusedMaxSlots];
+        // The dirty-row mover.  The slot lists go to LDS as 32-bit values (the host takes
+        // this path only for pools of fewer than 2^31 slots) and into two hash sets, so
+        // the dirty test is O(n): row i is dirty iff src[i] is in the destination set or
+        // dst[i] in the source set.  About 10 KB of LDS per workgroup still lets a CU
+        // hold 8 of them.
+        __shared__ int32_t s_src[kFusedMaxSlots], s_dst[kFusedMaxSlots];
+        __shared__ int32_t h_src[kFusedHash], h_dst[kFusedHash];
         __shared__ uint8_t dirty[kFusedMaxSlots];
-        const int32_t n4 = (n + 3) & ~3;
+        for (int32_t k = threadIdx.x; k < kFusedHash; k += kMoveThreads) {
+            h_src[k] = -1;
+            h_dst[k] = -1;
+        }
         int bad = 0;
-        for (int32_t k = threadIdx.x; k < n4; k += kMoveThreads) {
-            const int64_t a = k < n ? src[k] : -1, b = k < n ? dst[k] : -1;
-            if (k < n) bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
+        for (int32_t k = threadIdx.x; k < n; k += kMoveThreads) {
+            const int64_t a = src[k], b = dst[k];
+            bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
             s_src[k] = static_cast<int32_t>(a);
             s_dst[k] = static_cast<int32_t>(b);
         }
@@ -253,16 +293,14 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
             if (threadIdx.x == 0) set_status(status, TV_STATUS_BAD_SLOT);
             return;
         }
+        for (int32_t k = threadIdx.x; k < n; k += kMoveThreads) {
+            hash_insert(h_src, s_src[k]);
+            hash_insert(h_dst, s_dst[k]);
+        }
+        __syncthreads();
         int any = 0;
         for (int32_t i = threadIdx.x; i < n; i += kMoveThreads) {
-            const int32_t a = s_src[i], b = s_dst[i];
-            int d = 0;
-            for (int32_t k = 0; k < n4; k += 4) {
-                const int4 dk = *reinterpret_cast<const int4*>(&s_dst[k]);
-                const int4 sk = *reinterpret_cast<const int4*>(&s_src[k]);
-                d |= (a == dk.x) | (a == dk.y) | (a == dk.z) | (a == dk.w) | (b == sk.x) | (b == sk.y) |
-                     (b == sk.z) | (b == sk.w);
-            }
+            const int d = hash_contains(h_dst, s_src[i]) || hash_contains(h_src, s_dst[i]);
             dirty[i] = static_cast<uint8_t>(d);
             any |= d;
         }
