@@ -248,40 +248,28 @@ def accept_leg(batch, torch, steps: int, warmup: int, vocab: int = 151936) -> di
 def graph_leg(batch, torch, steps: int, warmup: int, layers: int = 36) -> dict:
     """A verify round's attention part for all 36 Qwen3-8B layers, eager vs one HIP-graph replay.
 
-    Per layer: the fused RoPE + scatter and the packed attention.  The eager path is the
-    serving call sequence (host plan cached per metadata object, one Python call per
-    kernel); the graph path plans on the device once per round (target_graph) and is
-    replayed as a whole, so the same graph stays valid while prefix lengths change.  Every
-    layer reuses the batch's pool and inputs (the work per layer is the same; 36 distinct
-    pools of config 4 would not fit the memory twice).  Wall-clock per round, host launch
-    cost included: the quantity a graph removes."""
+    Per layer: the fused RoPE + scatter and the drop-in packed attention, called the way
+    models/qwen3.py:223-240 calls them.  The graph is the reference runner's form
+    (target_graph.py:135-167): the same calls captured once against the round's metadata and
+    replayed; under capture the attention plans on the device, so the graph stays valid while
+    prefix lengths, trees and node counts change.  Every layer reuses the batch's pool and
+    inputs (the work per layer is the same; 36 distinct pools of config 4 would not fit the
+    memory twice).  Wall-clock per round, host launch cost included: the quantity a graph
+    removes."""
     from jetspec_amd import packed_tree_attention, rope_scatter_prevalidated, workloads
-    from jetspec_amd.target_graph import GraphedTreeAttention
 
     meta = batch.metadata
     positions = torch.tensor([meta.prefix_lengths[r] + d for r in range(meta.num_requests)
                               for d in workloads.depths_of(batch.parents[r])], dtype=torch.int32, device="cuda")
     cache = rope_cache(torch)
-    rotated = torch.empty_like(batch.q)
-    out = torch.empty_like(batch.q)
-    attention = GraphedTreeAttention(meta.node_counts_host, batch.k_pool.shape[2], meta.block_size,
-                                     max_prefix=max(meta.prefix_lengths), device="cuda")
 
-    def rope():
-        rope_scatter_prevalidated(batch.q, batch.new_k, batch.new_v, positions, cache, batch.k_pool, batch.v_pool,
-                                  meta.tree_slots, rotated)
-
-    def eager():
+    def round_():
+        out = None
         for _ in range(layers):
-            rope()
-            result = packed_tree_attention(rotated, batch.k_pool, batch.v_pool, meta, batch.scale, batch.groups)
-        return result
-
-    def graphed():
-        attention.prepare(meta)
-        for _ in range(layers):
-            rope()
-            attention(rotated, batch.k_pool, batch.v_pool, meta, batch.scale, out, prepared=True)
+            rotated = rope_scatter_prevalidated(batch.q, batch.new_k, batch.new_v, positions, cache, batch.k_pool,
+                                                batch.v_pool, meta.tree_slots, torch.empty_like(batch.q))
+            out = packed_tree_attention(rotated, batch.k_pool, batch.v_pool, meta, batch.scale, batch.groups)
+        return out
 
     def wall(fn, rounds):
         for _ in range(2):
@@ -294,19 +282,19 @@ def graph_leg(batch, torch, steps: int, warmup: int, layers: int = 36) -> dict:
         return (time.perf_counter() - t0) * 1e3 / rounds
 
     rounds = max(3, min(steps, 20))
-    eager_ms = wall(eager, rounds)
-    expected = eager()
+    eager_ms = wall(round_, rounds)
+    expected = round_()
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        graphed()
+        round_()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        graphed()
+        captured = round_()
     replay_ms = wall(graph.replay, rounds)
-    same = bool(torch.equal(out.view(torch.int16), expected.view(torch.int16)))
+    same = bool(torch.equal(captured.view(torch.int16), expected.view(torch.int16)))
     return {"layers": layers, "eager_ms_per_round": eager_ms, "graph_replay_ms_per_round": replay_ms,
             "speedup": eager_ms / replay_ms, "bitwise_equal": same}
 
