@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define TV_ABI_VERSION 3
+#define TV_ABI_VERSION 4
 
 enum tv_error {
     TV_OK = 0,
@@ -251,6 +251,8 @@ int tv_truncate_accepted(const int32_t* paths, int32_t path_stride, const int32_
  * copies (PackedTreeMetadata.prefix_lengths / node_counts_host).
  * Call once with NULL outputs to learn the sizes (written to *info), then again
  * with buffers of at least info->num_items * 8 and info->num_groups * 8 int32.
+ *   queries_per_kv: query heads per KV head, G (1, 2, 4, 8 or 16); a work item holds
+ *               256 score rows = (8 / HPW) * (32 / G) nodes x G heads x HPW KV heads.
  *   num_compute_units: CUs of the target device (256 on MI355X).
  *   chunk_keys: 0 = automatic; > 0 forces every prefix chunk to that many keys
  *               (a multiple of 32), which makes per-request results independent
@@ -265,7 +267,8 @@ typedef struct tv_attention_plan_info {
 } tv_attention_plan_info;
 
 int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
-                           int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                           int32_t num_requests, int32_t num_kv_heads, int32_t queries_per_kv,
+                           int32_t block_size,
                            int32_t num_compute_units, int32_t chunk_keys,
                            int32_t* items_host, int32_t* groups_host,
                            tv_attention_plan_info* info);
@@ -277,7 +280,7 @@ int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_
  * kernel, paged_backend.py:343-348.
  */
 int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
-                                 int32_t num_requests, int32_t num_kv_heads,
+                                 int32_t num_requests, int32_t num_kv_heads, int32_t queries_per_kv,
                                  int32_t num_compute_units, int32_t chunk_keys,
                                  int32_t* items_host, int32_t* groups_host,
                                  tv_attention_plan_info* info);
@@ -297,11 +300,13 @@ int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t*
  * it writes zero counts and error 1 instead of overrunning the arrays.
  */
 int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, int32_t num_requests,
-                                    int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
-                                    int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info);
+                                    int32_t num_kv_heads, int32_t queries_per_kv, int32_t block_size,
+                                    int32_t num_compute_units, int32_t chunk_keys, int64_t max_prefix,
+                                    tv_attention_plan_info* info);
 
 int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* node_counts,
-                                  int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                  int32_t num_requests, int32_t num_kv_heads, int32_t queries_per_kv,
+                                  int32_t block_size,
                                   int32_t num_compute_units, int32_t chunk_keys, int32_t item_capacity,
                                   int32_t group_capacity, int32_t slot_capacity, int32_t* items,
                                   int32_t* groups, int32_t* counts, void* stream);
@@ -314,11 +319,13 @@ int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* nod
  * PackedTargetGraph replays one captured graph for all of them (target_graph.py:150-167),
  * so a captured launch must be sized for the whole class:
  *     max T <= min(1024, Q - (R - 1), floor(sqrt(sum T^2)))
- *     node blocks <= Hkv * min((Q + 63 R) / 64, R * ceil(max T / 64)).
+ *     node blocks <= Hkv * min((Q + (N - 1) R) / N, R * ceil(max T / N)),
+ * N = 256 / queries_per_kv nodes per one-head work item.
  */
 int tv_tree_attention_plan_capacity_packed(int32_t total_queries, int32_t num_requests,
                                            int64_t sum_node_squares, int32_t num_kv_heads,
-                                           int32_t block_size, int32_t num_compute_units,
+                                           int32_t queries_per_kv, int32_t block_size,
+                                           int32_t num_compute_units,
                                            int32_t chunk_keys, int64_t max_prefix,
                                            tv_attention_plan_info* info);
 
@@ -435,8 +442,10 @@ typedef struct tv_tree_attention_args {
  * whose ancestor bit is set (addressed through tree_slots).  bf16/f16 operands,
  * fp32 accumulation and online softmax, probabilities rounded to the operand
  * type for the P.V product (tree_gqa.py:102-105).
- * Implemented geometry: head_dim 128, num_q_heads == 4 * num_kv_heads,
- * block_size % 32 == 0 (any positive block_size with prefix_slots).
+ * Implemented geometry: head_dim 128, num_q_heads == G * num_kv_heads with G in
+ * {1, 2, 4, 8, 16} (the reference's grouped kernel takes powers of two up to 16,
+ * tree_gqa.py:124-126), block_size % 32 == 0 (any positive block_size with
+ * prefix_slots).  The plan must have been made for the same G.
  */
 int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
 

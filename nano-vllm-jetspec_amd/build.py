@@ -3,11 +3,14 @@
     python nano-vllm-jetspec_amd/build.py [--verbose]
 
 The library lands next to the Python package (jetspec_amd/libtreeverify.so), which
-is where jetspec_amd._lib loads it from.  Every call recompiles.
+is where jetspec_amd._lib loads it from.  Every call recompiles: each source is
+compiled to an object in parallel (the attention kernel is instantiated per query
+group in its own translation unit), then the objects are linked.
 """
 from __future__ import annotations
 
 import argparse
+from concurrent.futures import ThreadPoolExecutor
 import os
 from pathlib import Path
 import shutil
@@ -20,16 +23,39 @@ CSRC = HERE / "csrc"
 OUTPUT = HERE / "jetspec_amd" / "libtreeverify.so"
 ARCH = "gfx950"
 
-SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", "tv_rope.hip", "tv_accept.hip", "tv_metadata.hip", "tv_plan_device.hip")
+# Query heads per KV head the attention kernel is instantiated for.
+GROUPS = (1, 2, 4, 8, 16)
+ATTENTION_GROUP_SOURCES = tuple(f"tv_attention_g{g}.hip" for g in GROUPS)
+SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", *ATTENTION_GROUP_SOURCES,
+           "tv_rope.hip", "tv_accept.hip", "tv_metadata.hip", "tv_plan_device.hip")
 
 # Packed-FP32 VALU instructions are kept out of the device code (they are not
 # needed: the hot loops are MFMA and single-precision VALU work).
 HIP_FLAGS = (
-    "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-O3", "-std=c++17", "-fPIC",
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 )
+# hipcc's host pass does not know the packed-fp32 feature flag and says so; that
+# warning is expected and filtered out of the report.
+NOISE = "'-packed-fp32-ops' is not a recognized feature"
+
+
+def _jobs() -> int:
+    try:
+        requested = int(os.environ.get("MAX_JOBS", "0"))
+    except ValueError:
+        requested = 0
+    return max(1, min(requested or (os.cpu_count() or 1), 16, len(SOURCES)))
+
+
+def _run(cmd: list[str], what: str) -> list[str]:
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    messages = [line for line in (result.stdout + result.stderr).splitlines() if NOISE not in line]
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {what}:\n" + "\n".join(messages))
+    return messages
 
 
 def hipcc() -> str:
@@ -39,55 +65,64 @@ def hipcc() -> str:
     return path
 
 
-def check_m0_discipline(verbose: bool = False) -> None:
+def _check_m0(source: str, tmp: Path) -> None:
+    import re
+
+    asm = tmp / (Path(source).stem + ".s")
+    cmd = [hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-S", "--cuda-device-only",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{REPO / 'include'}",
+           f"-I{CSRC}", str(CSRC / source), "-o", str(asm)]
+    _run(cmd, source + " (-S)")
+    # Explicit M0 operands other than the DMA's own writes, and the instructions that
+    # read M0 implicitly (indexed register moves).
+    implicit = re.compile(r"^\s*(s_set_gpr_idx_on|s_movrel|v_movrel)")
+    bad = [line.strip() for line in asm.read_text().splitlines()
+           if not line.lstrip().startswith(";")
+           and ((re.search(r"\bm0\b", line) and not re.match(r"\s*s_mov_b32 m0, s\d+\s*$", line))
+                or implicit.match(line))]
+    if bad:
+        raise RuntimeError(f"{source}: compiler-generated M0 use would be clobbered by the DMA asm: "
+                           + "; ".join(bad[:5]))
+
+
+def check_m0_discipline(verbose: bool = False, jobs: int | None = None) -> None:
     """The attention kernel issues its global->LDS DMA from inline asm that sets M0.
 
     That is only sound while no compiler-generated instruction of the kernel uses M0,
-    so compile the device code to assembly and require every M0 reference to be one
-    of those `s_mov_b32 m0, sN` writes.
+    so compile each translation unit holding an instance of the kernel to assembly and
+    require every M0 reference to be one of those `s_mov_b32 m0, sN` writes.
     """
-    import re
     import tempfile
 
-    with tempfile.TemporaryDirectory() as tmp:
-        asm = Path(tmp) / "tv_attention.s"
-        cmd = [hipcc(), "-O3", "-std=c++17", f"--offload-arch={ARCH}", "-S", "--cuda-device-only",
-               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", f"-I{REPO / 'include'}",
-               f"-I{CSRC}", str(CSRC / "tv_attention.hip"), "-o", str(asm)]
-        result = subprocess.run(cmd, capture_output=True, text=True)
-        if result.returncode != 0:
-            raise RuntimeError("hipcc -S failed:\n" + result.stderr)
-        # Explicit M0 operands other than the DMA's own writes, and the instructions that
-        # read M0 implicitly (indexed register moves).
-        implicit = re.compile(r"^\s*(s_set_gpr_idx_on|s_movrel|v_movrel)")
-        bad = [line.strip() for line in asm.read_text().splitlines()
-               if not line.lstrip().startswith(";")
-               and ((re.search(r"\bm0\b", line) and not re.match(r"\s*s_mov_b32 m0, s\d+\s*$", line))
-                    or implicit.match(line))]
-        if bad:
-            raise RuntimeError("compiler-generated M0 use would be clobbered by the DMA asm: " + "; ".join(bad[:5]))
-        if verbose:
-            print("M0 discipline ok", flush=True)
+    with tempfile.TemporaryDirectory() as tmp, ThreadPoolExecutor(jobs or _jobs()) as pool:
+        list(pool.map(lambda src: _check_m0(src, Path(tmp)), ATTENTION_GROUP_SOURCES))
+    if verbose:
+        print("M0 discipline ok", flush=True)
 
 
 def build(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
-    tmp = OUTPUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIP_FLAGS, *extra_flags, f"-I{REPO / 'include'}", f"-I{CSRC}",
-           *[str(CSRC / name) for name in SOURCES], "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    env = dict(os.environ)
-    result = subprocess.run(cmd, capture_output=True, text=True, env=env)
-    # hipcc's host pass does not know the packed-fp32 feature flag and says so; that
-    # warning is expected and filtered out of the report.
-    noise = "'-packed-fp32-ops' is not a recognized feature"
-    messages = [line for line in (result.stdout + result.stderr).splitlines() if noise not in line]
-    if result.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + "\n".join(messages))
+    import tempfile
+
+    tmp_so = OUTPUT.with_suffix(".so.tmp")
+    jobs = _jobs()
+    with tempfile.TemporaryDirectory() as tmp:
+        objects = [Path(tmp) / (name.replace(".", "_") + ".o") for name in SOURCES]
+
+        def compile_one(index: int) -> list[str]:
+            cmd = [hipcc(), *HIP_FLAGS, *extra_flags, f"-I{REPO / 'include'}", f"-I{CSRC}", "-c",
+                   str(CSRC / SOURCES[index]), "-o", str(objects[index])]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            return _run(cmd, SOURCES[index])
+
+        with ThreadPoolExecutor(jobs) as pool:
+            messages = [line for lines in pool.map(compile_one, range(len(SOURCES))) for line in lines]
+        link = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objects), "-o", str(tmp_so)]
+        messages += _run(link, "link")
     if verbose and messages:
         print("\n".join(messages), flush=True)
-    check_m0_discipline(verbose)
-    os.replace(tmp, OUTPUT)
+    check_m0_discipline(verbose, jobs)
+    os.replace(tmp_so, OUTPUT)
     return OUTPUT
 
 

@@ -58,21 +58,24 @@ argmax_rows_kernel(const S* __restrict__ logits, int64_t row_stride, int64_t voc
     };
     // Full vector units first (VEC elements each), then the scalar tail.
     const int64_t units = VEC > 1 ? vocab / VEC : 0;
-    for (int64_t u0 = threadIdx.x; u0 < units; u0 += kUnroll * kArgmaxThreads) {
-        u32x4 raw[kUnroll];
+    if constexpr (VEC > 1) {
+        static_assert(VEC * sizeof(S) == sizeof(u32x4), "a vector unit is one 16-byte load");
+        for (int64_t u0 = threadIdx.x; u0 < units; u0 += kUnroll * kArgmaxThreads) {
+            u32x4 raw[kUnroll];
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) {
-            const int64_t u = u0 + k * kArgmaxThreads;
-            if (u < units) raw[k] = *reinterpret_cast<const u32x4*>(base + u * VEC);
-        }
+            for (int k = 0; k < kUnroll; ++k) {
+                const int64_t u = u0 + k * kArgmaxThreads;
+                if (u < units) raw[k] = *reinterpret_cast<const u32x4*>(base + u * VEC);
+            }
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) {
-            const int64_t u = u0 + k * kArgmaxThreads;
-            if (u < units) {
-                S vals[VEC];
-                __builtin_memcpy(vals, &raw[k], 16);
+            for (int k = 0; k < kUnroll; ++k) {
+                const int64_t u = u0 + k * kArgmaxThreads;
+                if (u < units) {
+                    S vals[VEC];
+                    __builtin_memcpy(vals, &raw[k], sizeof(vals));
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) visit(elem_value(vals, e), u * VEC + e);
+                    for (int e = 0; e < VEC; ++e) visit(elem_value(vals, e), u * VEC + e);
+                }
             }
         }
     }

@@ -4,8 +4,8 @@
 // (paged_backend.py:290) or per (4-node block, KV head) (tree_gqa.py:130), and every
 // program walks its request's whole prefix.  On MI355X the kernel instead gives a
 // 512-thread workgroup 256 score rows that share one K/V stream:
-//   HPW (KV heads per workgroup) = 2 / 1 for trees of <=32 / >32 nodes,
-//   NPW (nodes per workgroup)    = 64 / HPW,
+//   NPW (nodes per workgroup)    = (8 / HPW) * (32 / G) for G query heads per KV head,
+//   HPW (KV heads per workgroup) = 2 for trees that fit NPW(2) nodes (32 at G = 4), else 1,
 // so a KV tile staged in LDS is reused by every (node, query head) row of its group.
 // Long prefixes are cut into chunks (split-K) only as far as needed to give every
 // compute unit work; items are ordered longest first so the hardware dispatcher's
@@ -39,8 +39,15 @@ struct Item {
     int32_t hg, chunk, nb;
 };
 
-int heads_per_group(int32_t nodes, int32_t kv_heads) {
-    int h = nodes <= 32 ? 2 : 1;
+// A wave owns 32 score rows = 32 / qpk nodes x qpk query heads, so a workgroup of 8 waves
+// holds (8 / hpw) * (32 / qpk) nodes of each of its hpw KV heads; trees that fit the
+// two-head form (<= 32 nodes at qpk 4) take it.
+int nodes_per_item(int hpw, int32_t qpk) { return (8 / hpw) * (32 / qpk); }
+
+bool supported_group(int32_t qpk) { return qpk == 1 || qpk == 2 || qpk == 4 || qpk == 8 || qpk == 16; }
+
+int heads_per_group(int32_t nodes, int32_t kv_heads, int32_t qpk) {
+    int h = nodes <= nodes_per_item(2, qpk) ? 2 : 1;
     while (h > 1 && h > kv_heads) h >>= 1;
     return h;
 }
@@ -148,11 +155,14 @@ void place_for_xcds(std::vector<Item>& items) {
 
 // The plan for chunks of at most max_chunk keys (a multiple of 32).
 int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32_t num_requests,
-         int32_t num_kv_heads, int32_t num_compute_units, int32_t chunk_keys, int64_t max_chunk,
+         int32_t num_kv_heads, int32_t qpk, int32_t num_compute_units, int32_t chunk_keys, int64_t max_chunk,
          int32_t* items_host, int32_t* groups_host, tv_attention_plan_info* info) {
     if (!info || !prefix_lens_host || !node_counts_host) return fail(TV_ERR_INVALID, "plan: null argument");
     if (num_requests < 1) return fail(TV_ERR_INVALID, "plan: at least one request is required");
     if (num_kv_heads < 1) return fail(TV_ERR_INVALID, "plan: num_kv_heads must be positive");
+    if (!supported_group(qpk)) {
+        return fail(TV_ERR_UNSUPPORTED, "plan: %d query heads per KV head (implemented: 1, 2, 4, 8 or 16)", qpk);
+    }
     if (num_compute_units < 1) return fail(TV_ERR_INVALID, "plan: num_compute_units must be positive");
     if (chunk_keys < 0 || chunk_keys % 32) {
         return fail(TV_ERR_INVALID, "plan: chunk_keys %d must be a non-negative multiple of 32", chunk_keys);
@@ -168,8 +178,8 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
                         kMaxTreeNodes);
         }
         max_nodes = std::max(max_nodes, t);
-        const int hpw = heads_per_group(t, num_kv_heads);
-        const int npw = 64 / hpw;
+        const int hpw = heads_per_group(t, num_kv_heads, qpk);
+        const int npw = nodes_per_item(hpw, qpk);
         const int64_t groups = (num_kv_heads + hpw - 1) / hpw;
         const int64_t blocks = (t + npw - 1) / npw;
         total_cost += groups * blocks * cost_weight(hpw) * (static_cast<int64_t>(p) + t);
@@ -192,8 +202,8 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
         int64_t n = 0;
         for (int32_t r = 0; r < num_requests; ++r) {
             const int64_t p = prefix_lens_host[r];
-            const int hpw = heads_per_group(node_counts_host[r], num_kv_heads);
-            const int npw = 64 / hpw;
+            const int hpw = heads_per_group(node_counts_host[r], num_kv_heads, qpk);
+            const int npw = nodes_per_item(hpw, qpk);
             const int64_t units = static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((node_counts_host[r] + npw - 1) / npw);
             const int64_t chunk = chunk_for(p, hpw, tau);
             n += units * (p > 0 ? (p + chunk - 1) / chunk : 1);
@@ -218,8 +228,8 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
     int32_t num_slots = 0, num_groups = 0;
     for (int32_t r = 0; r < num_requests; ++r) {
         const int32_t p = prefix_lens_host[r], t = node_counts_host[r];
-        const int hpw = heads_per_group(t, num_kv_heads);
-        const int npw = 64 / hpw;
+        const int hpw = heads_per_group(t, num_kv_heads, qpk);
+        const int npw = nodes_per_item(hpw, qpk);
         const int32_t groups = (num_kv_heads + hpw - 1) / hpw;
         const int32_t blocks = (t + npw - 1) / npw;
         const int64_t chunk = chunk_keys > 0 ? chunk_keys : chunk_for(p, hpw, tau);
@@ -300,7 +310,8 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
 using namespace tv;
 
 extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
-                                      int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                      int32_t num_requests, int32_t num_kv_heads, int32_t queries_per_kv,
+                                      int32_t block_size,
                                       int32_t num_compute_units, int32_t chunk_keys, int32_t* items_host,
                                       int32_t* groups_host, tv_attention_plan_info* info) {
     clear_error();
@@ -309,15 +320,16 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
     }
     // Longest chunk whose pages fit the LDS page cache wherever it starts.
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
-    return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, num_compute_units, chunk_keys,
-                max_chunk, items_host, groups_host, info);
+    return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, queries_per_kv, num_compute_units,
+                chunk_keys, max_chunk, items_host, groups_host, info);
 }
 
 extern "C" int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
-                                            int32_t num_requests, int32_t num_kv_heads, int32_t num_compute_units,
+                                            int32_t num_requests, int32_t num_kv_heads, int32_t queries_per_kv,
+                                            int32_t num_compute_units,
                                             int32_t chunk_keys, int32_t* items_host, int32_t* groups_host,
                                             tv_attention_plan_info* info) {
     clear_error();
-    return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, num_compute_units, chunk_keys,
-                kMaxSlotChunk, items_host, groups_host, info);
+    return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, queries_per_kv, num_compute_units,
+                chunk_keys, kMaxSlotChunk, items_host, groups_host, info);
 }

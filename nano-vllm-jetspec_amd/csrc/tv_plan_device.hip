@@ -38,15 +38,18 @@ constexpr int64_t kFillRounds = 4;
 struct PlanArgs {
     const int32_t* prefix_lens;
     const int32_t* node_counts;
-    int32_t num_requests, num_kv_heads, block_size, compute_units, chunk_keys;
+    int32_t num_requests, num_kv_heads, qpk, block_size, compute_units, chunk_keys;
     int32_t item_capacity, group_capacity, slot_capacity;
     int32_t* items;      // [item_capacity, 8]
     int32_t* groups;     // [group_capacity, 8]
     int32_t* counts;     // [4]: items, groups, partial slots, error
 };
 
-__device__ __forceinline__ int heads_per_group(int nodes, int kv_heads) {
-    int h = nodes <= 32 ? 2 : 1;
+// Nodes of one KV head per work item and the two-head rule of the host planner (tv_plan.cpp).
+__host__ __device__ __forceinline__ int nodes_per_item(int hpw, int qpk) { return (8 / hpw) * (32 / qpk); }
+
+__device__ __forceinline__ int heads_per_group(int nodes, int kv_heads, int qpk) {
+    int h = nodes <= nodes_per_item(2, qpk) ? 2 : 1;
     while (h > 1 && h > kv_heads) h >>= 1;
     return h;
 }
@@ -119,8 +122,8 @@ plan_device_kernel(const PlanArgs a) {
             bad = true;
             continue;
         }
-        const int hpw = heads_per_group(n, a.num_kv_heads);
-        const int npw = 64 / hpw;
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
+        const int npw = nodes_per_item(hpw, a.qpk);
         const int64_t groups = (a.num_kv_heads + hpw - 1) / hpw;
         const int64_t blocks = (n + npw - 1) / npw;
         my_cost += groups * blocks * cost_weight(hpw) * (static_cast<int64_t>(p) + n);
@@ -141,8 +144,8 @@ plan_device_kernel(const PlanArgs a) {
         for (int r = t; r < R; r += kPlanThreads) {
             const int64_t p = max(0, a.prefix_lens[r]);
             const int nodes = max(1, min(1024, a.node_counts[r]));
-            const int hpw = heads_per_group(nodes, a.num_kv_heads);
-            const int npw = 64 / hpw;
+            const int hpw = heads_per_group(nodes, a.num_kv_heads, a.qpk);
+            const int npw = nodes_per_item(hpw, a.qpk);
             const int64_t units = static_cast<int64_t>((a.num_kv_heads + hpw - 1) / hpw) * ((nodes + npw - 1) / npw);
             const int64_t chunk = chunk_for(p, hpw, tau, max_chunk);
             n += units * (p > 0 ? (p + chunk - 1) / chunk : 1);
@@ -171,8 +174,8 @@ plan_device_kernel(const PlanArgs a) {
     for (int r = r0; r < r1; ++r) {
         const int p = max(0, a.prefix_lens[r]);
         const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
-        const int npw = 64 / hpw;
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
+        const int npw = nodes_per_item(hpw, a.qpk);
         const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
         const int64_t NB = (n + npw - 1) / npw;
         const int64_t chunk = a.chunk_keys > 0 ? a.chunk_keys : chunk_for(p, hpw, tau, max_chunk);
@@ -190,9 +193,9 @@ plan_device_kernel(const PlanArgs a) {
     int64_t slot_base = block_scan(my_slots, scan, &totals[3]);
     for (int r = r0; r < r1; ++r) {
         const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
         const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int64_t NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int64_t NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
         req_item_off[r] = static_cast<int32_t>(item_base);
         req_group_off[r] = static_cast<int32_t>(group_base);
         req_slot_off[r] = static_cast<int32_t>(slot_base);
@@ -225,9 +228,9 @@ plan_device_kernel(const PlanArgs a) {
     for (int r = r0; r < r1; ++r) {
         const int p = max(0, a.prefix_lens[r]);
         const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
         const int G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
         const int nc = req_nchunks[r];
         const int64_t chunk = req_chunk[r];
         for (int hg = 0; hg < G; ++hg) {
@@ -271,8 +274,8 @@ plan_device_kernel(const PlanArgs a) {
         const int r = lo;
         const int p = max(0, a.prefix_lens[r]);
         const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
-        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
+        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
         const int nc = req_nchunks[r];
         const int64_t local = idx - req_item_off[r];
         const int nb = static_cast<int>(local % NB);
@@ -282,7 +285,7 @@ plan_device_kernel(const PlanArgs a) {
         const int64_t chunk = req_chunk[r];
         out[0] = r;
         out[1] = hg * hpw;
-        out[2] = nb * (64 / hpw);
+        out[2] = nb * nodes_per_item(hpw, a.qpk);
         out[3] = static_cast<int32_t>(min(static_cast<int64_t>(p), c * chunk));
         out[4] = static_cast<int32_t>(min(static_cast<int64_t>(p), (c + 1) * chunk));
         out[5] = c == nc - 1 ? 1 : 0;
@@ -298,8 +301,8 @@ plan_device_kernel(const PlanArgs a) {
             if (req_item_off[mid] <= idx) lo = mid; else hi = mid - 1;
         }
         const int n = max(1, min(1024, a.node_counts[lo]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
-        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
+        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
         return (static_cast<int64_t>(lo) << 32) | ((idx - req_item_off[lo]) / NB);
     };
 
@@ -317,8 +320,8 @@ plan_device_kernel(const PlanArgs a) {
     }
     for (int r = t; r < R; r += kPlanThreads) {
         const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
-        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
+        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
         if (NB > 1 && NB % kXcds) atomicOr(&shared_flag, 2);
     }
     __syncthreads();
@@ -404,15 +407,15 @@ plan_device_kernel(const PlanArgs a) {
         const int nc = req_nchunks[r];
         if (nc < 2) continue;
         const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads);
+        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
         const int G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int NB = (n + 64 / hpw - 1) / (64 / hpw);
+        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
         for (int hg = 0; hg < G; ++hg) {
             for (int nb = 0; nb < NB; ++nb) {
                 int32_t* gr = a.groups + static_cast<int64_t>(req_group_off[r] + hg * NB + nb) * 8;
                 gr[0] = r;
                 gr[1] = hg * hpw;
-                gr[2] = nb * (64 / hpw);
+                gr[2] = nb * nodes_per_item(hpw, a.qpk);
                 gr[3] = hpw;
                 gr[4] = req_slot_off[r] + (hg * NB + nb) * nc;
                 gr[5] = nc;
@@ -461,21 +464,25 @@ int fill_capacity(int64_t blocks, int32_t max_nodes, int32_t block_size, int32_t
     return TV_OK;
 }
 
-bool capacity_args_ok(int32_t num_requests, int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
-                      int32_t chunk_keys, int64_t max_prefix) {
-    return num_requests >= 1 && num_kv_heads >= 1 && block_size >= 32 && block_size % 32 == 0 &&
-           num_compute_units >= 1 && max_prefix >= 0 && chunk_keys >= 0 && chunk_keys % 32 == 0;
+bool supported_group(int32_t qpk) { return qpk == 1 || qpk == 2 || qpk == 4 || qpk == 8 || qpk == 16; }
+
+bool capacity_args_ok(int32_t num_requests, int32_t num_kv_heads, int32_t qpk, int32_t block_size,
+                      int32_t num_compute_units, int32_t chunk_keys, int64_t max_prefix) {
+    return num_requests >= 1 && num_kv_heads >= 1 && supported_group(qpk) && block_size >= 32 &&
+           block_size % 32 == 0 && num_compute_units >= 1 && max_prefix >= 0 && chunk_keys >= 0 && chunk_keys % 32 == 0;
 }
 
 }  // namespace
 }  // namespace tv
 
 extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, int32_t num_requests,
-                                               int32_t num_kv_heads, int32_t block_size, int32_t num_compute_units,
-                                               int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info) {
+                                               int32_t num_kv_heads, int32_t queries_per_kv, int32_t block_size,
+                                               int32_t num_compute_units, int32_t chunk_keys, int64_t max_prefix,
+                                               tv_attention_plan_info* info) {
     clear_error();
+    const int32_t qpk = queries_per_kv;
     if (!node_counts_host || !info ||
-        !capacity_args_ok(num_requests, num_kv_heads, block_size, num_compute_units, chunk_keys, max_prefix)) {
+        !capacity_args_ok(num_requests, num_kv_heads, qpk, block_size, num_compute_units, chunk_keys, max_prefix)) {
         return fail(TV_ERR_INVALID, "plan_capacity: invalid arguments");
     }
     if (num_requests > kMaxPlanRequests) {
@@ -487,8 +494,8 @@ extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, 
         const int32_t n = node_counts_host[r];
         if (n < 1 || n > 1024) return fail(TV_ERR_UNSUPPORTED, "plan_capacity: request %d has %d nodes", r, n);
         max_nodes = n > max_nodes ? n : max_nodes;
-        const int hpw = n <= 32 && num_kv_heads >= 2 ? 2 : 1;
-        const int npw = 64 / hpw;
+        const int hpw = n <= nodes_per_item(2, qpk) && num_kv_heads >= 2 ? 2 : 1;
+        const int npw = nodes_per_item(hpw, qpk);
         blocks += static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((n + npw - 1) / npw);
     }
     return fill_capacity(blocks, max_nodes, block_size, num_compute_units, chunk_keys, max_prefix, info);
@@ -496,12 +503,13 @@ extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, 
 
 extern "C" int tv_tree_attention_plan_capacity_packed(int32_t total_queries, int32_t num_requests,
                                                       int64_t sum_node_squares, int32_t num_kv_heads,
-                                                      int32_t block_size, int32_t num_compute_units,
-                                                      int32_t chunk_keys, int64_t max_prefix,
-                                                      tv_attention_plan_info* info) {
+                                                      int32_t queries_per_kv, int32_t block_size,
+                                                      int32_t num_compute_units, int32_t chunk_keys,
+                                                      int64_t max_prefix, tv_attention_plan_info* info) {
     clear_error();
+    const int32_t qpk = queries_per_kv;
     if (!info || total_queries < num_requests ||
-        !capacity_args_ok(num_requests, num_kv_heads, block_size, num_compute_units, chunk_keys, max_prefix)) {
+        !capacity_args_ok(num_requests, num_kv_heads, qpk, block_size, num_compute_units, chunk_keys, max_prefix)) {
         return fail(TV_ERR_INVALID, "plan_capacity_packed: invalid arguments");
     }
     if (num_requests > kMaxPlanRequests) {
@@ -517,11 +525,13 @@ extern "C" int tv_tree_attention_plan_capacity_packed(int32_t total_queries, int
         max_nodes = std::min(max_nodes, root);
     }
     max_nodes = std::min<int64_t>(max_nodes, 1024);
-    // A request of T nodes has at most num_kv_heads * ceil(T / 64) node blocks (two-head
-    // groups of trees of <= 32 nodes have fewer), and sum_r ceil(T_r / 64) is at most
-    // (Q + 63 R) / 64 and at most R * ceil(max T / 64).
-    const int64_t per_head = std::min<int64_t>((static_cast<int64_t>(total_queries) + 63 * num_requests) / 64,
-                                               static_cast<int64_t>(num_requests) * ((max_nodes + 63) / 64));
+    // With N = nodes_per_item(1, qpk) nodes per one-head item (64 at qpk 4), a request of T
+    // nodes has at most num_kv_heads * ceil(T / N) node blocks (two-head groups of smaller
+    // trees have fewer), and sum_r ceil(T_r / N) is at most (Q + (N - 1) R) / N and at most
+    // R * ceil(max T / N).
+    const int64_t npw1 = nodes_per_item(1, qpk);
+    const int64_t per_head = std::min<int64_t>((static_cast<int64_t>(total_queries) + (npw1 - 1) * num_requests) / npw1,
+                                               static_cast<int64_t>(num_requests) * ((max_nodes + npw1 - 1) / npw1));
     const int64_t blocks = static_cast<int64_t>(num_kv_heads) * per_head;
     return fill_capacity(blocks, static_cast<int32_t>(max_nodes), block_size, num_compute_units, chunk_keys,
                          max_prefix, info);
@@ -542,12 +552,14 @@ extern "C" int tv_stream_capture_info(void* stream, int32_t* capturing, uint64_t
 }
 
 extern "C" int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* node_counts,
-                                             int32_t num_requests, int32_t num_kv_heads, int32_t block_size,
+                                             int32_t num_requests, int32_t num_kv_heads, int32_t queries_per_kv,
+                                             int32_t block_size,
                                              int32_t num_compute_units, int32_t chunk_keys, int32_t item_capacity,
                                              int32_t group_capacity, int32_t slot_capacity, int32_t* items,
                                              int32_t* groups, int32_t* counts, void* stream) {
     clear_error();
-    if (num_requests < 1 || num_requests > kMaxPlanRequests || num_kv_heads < 1 || block_size < 32 ||
+    if (num_requests < 1 || num_requests > kMaxPlanRequests || num_kv_heads < 1 || !supported_group(queries_per_kv) ||
+        block_size < 32 ||
         block_size % 32 || num_compute_units < 1 || chunk_keys < 0 || chunk_keys % 32 || item_capacity < 1 ||
         item_capacity > kMaxSortItems || group_capacity < 0 || slot_capacity < 0) {
         return fail(TV_ERR_INVALID, "plan_device: invalid arguments");
@@ -555,8 +567,8 @@ extern "C" int tv_tree_attention_plan_device(const int32_t* prefix_lens, const i
     if (!prefix_lens || !node_counts || !items || !counts || (group_capacity > 0 && !groups)) {
         return fail(TV_ERR_INVALID, "plan_device: null pointer");
     }
-    PlanArgs a{prefix_lens, node_counts, num_requests, num_kv_heads, block_size, num_compute_units, chunk_keys,
-               item_capacity, group_capacity, slot_capacity, items, groups, counts};
+    PlanArgs a{prefix_lens, node_counts, num_requests, num_kv_heads, queries_per_kv, block_size, num_compute_units,
+               chunk_keys, item_capacity, group_capacity, slot_capacity, items, groups, counts};
     hipLaunchKernelGGL(plan_device_kernel, dim3(1), dim3(kPlanThreads), 0, as_stream(stream), a);
     return check_launch("plan_device");
 }

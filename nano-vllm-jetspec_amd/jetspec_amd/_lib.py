@@ -12,7 +12,7 @@ from pathlib import Path
 import threading
 
 LIBRARY_PATH = Path(__file__).resolve().parent / "libtreeverify.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TV_OK = 0
 TV_ERR_INVALID = -1
@@ -163,11 +163,12 @@ def _declare(lib: ctypes.CDLL) -> None:
                                          c_void_p, c_void_p, c_void_p]
     lib.tv_tree_attention_plan.restype = c_int32
     lib.tv_tree_attention_plan.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32, c_int32,
-                                           c_int32, c_int32, POINTER(c_int32), POINTER(c_int32),
+                                           c_int32, c_int32, c_int32, POINTER(c_int32), POINTER(c_int32),
                                            POINTER(PlanInfo)]
     lib.tv_tree_attention_plan_slots.restype = c_int32
     lib.tv_tree_attention_plan_slots.argtypes = [POINTER(c_int32), POINTER(c_int32), c_int32, c_int32, c_int32,
-                                                 c_int32, POINTER(c_int32), POINTER(c_int32), POINTER(PlanInfo)]
+                                                 c_int32, c_int32, POINTER(c_int32), POINTER(c_int32),
+                                                 POINTER(PlanInfo)]
     lib.tv_pack_ancestor_words.restype = c_int32
     lib.tv_pack_ancestor_words.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
                                            c_int32, c_void_p, c_void_p, c_void_p]
@@ -191,13 +192,14 @@ def _declare(lib: ctypes.CDLL) -> None:
                                                 c_void_p, c_void_p]
     lib.tv_tree_attention_plan_capacity.restype = c_int32
     lib.tv_tree_attention_plan_capacity.argtypes = [POINTER(c_int32), c_int32, c_int32, c_int32, c_int32, c_int32,
-                                                    c_int64, POINTER(PlanInfo)]
+                                                    c_int32, c_int64, POINTER(PlanInfo)]
     lib.tv_tree_attention_plan_device.restype = c_int32
     lib.tv_tree_attention_plan_device.argtypes = [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
-                                                  c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]
+                                                  c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                                  c_void_p]
     lib.tv_tree_attention_plan_capacity_packed.restype = c_int32
     lib.tv_tree_attention_plan_capacity_packed.argtypes = [c_int32, c_int32, c_int64, c_int32, c_int32, c_int32,
-                                                           c_int32, c_int64, POINTER(PlanInfo)]
+                                                           c_int32, c_int32, c_int64, POINTER(PlanInfo)]
     lib.tv_stream_capture_info.restype = c_int32
     lib.tv_stream_capture_info.argtypes = [c_void_p, POINTER(c_int32), POINTER(c_uint64)]
     lib.tv_tree_accept.restype = c_int32

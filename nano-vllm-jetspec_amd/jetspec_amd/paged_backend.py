@@ -48,6 +48,9 @@ import torch
 from . import _device, _lib
 
 _BACKENDS = ("auto", "reference", "prefix", "gqa")
+# Query heads per KV head the kernel is built for (the reference's grouped kernel takes
+# powers of two up to 16, tree_gqa.py:124-126).
+SUPPORTED_GROUPS = (1, 2, 4, 8, 16)
 _derived: dict[int, dict] = {}
 _derived_lock = threading.Lock()
 
@@ -74,8 +77,9 @@ def _validate(q, k_pool, v_pool, metadata, groups, output_dtype) -> torch.dtype:
         raise ValueError("output dtype must match input or be FP32 for qualification")
     if q.dtype == torch.float32:
         raise ValueError("the MI355X tree-attention kernel takes bf16 or f16 operands (FP32 Q/K/V unsupported)")
-    if groups != 4 or q.shape[-1] != 128:
-        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 4 query heads per KV head")
+    if groups not in SUPPORTED_GROUPS or q.shape[-1] != 128:
+        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 1, 2, 4, 8 or 16 "
+                         "query heads per KV head")
     if metadata.block_size % 32:
         raise ValueError("the MI355X tree-attention kernel needs a page size that is a multiple of 32")
     return dtype
@@ -125,8 +129,8 @@ def _per_metadata(metadata) -> dict:
     return per_meta
 
 
-def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
-    """Work plan and ancestor bits of `metadata` for `num_kv_heads`, built once per object."""
+def derived_state(metadata, num_kv_heads: int, *, queries_per_kv: int, chunk_keys: int = 0) -> dict:
+    """Work plan and ancestor bits of `metadata` for one head geometry, built once per object."""
     per_meta = _per_metadata(metadata)
     lib = _lib.library()
     device = metadata.tree_slots.device
@@ -148,11 +152,11 @@ def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
             words.data_ptr(), status.data_ptr(), _device.stream_handle(device)), "pack_ancestor_words")
         per_meta["ancestor_words"] = words
         per_meta["words_per_row"] = per_row
-    plan_key = ("plan", int(num_kv_heads), int(chunk_keys))
+    plan_key = ("plan", int(num_kv_heads), int(queries_per_kv), int(chunk_keys))
     plan = per_meta.get(plan_key)
     if plan is None:
         plan = make_plan(metadata.prefix_lengths, metadata.node_counts_host, num_kv_heads, metadata.block_size,
-                         _device.compute_units(device.index), chunk_keys)
+                         _device.compute_units(device.index), chunk_keys, queries_per_kv=queries_per_kv)
         plan["items_dev"] = torch.from_numpy(plan["items"]).to(device, non_blocking=False)
         plan["groups_dev"] = (torch.from_numpy(plan["groups"]).to(device, non_blocking=False)
                               if plan["num_groups"] else None)
@@ -161,19 +165,20 @@ def derived_state(metadata, num_kv_heads: int, *, chunk_keys: int = 0) -> dict:
 
 
 def make_plan(prefix_lengths, node_counts, num_kv_heads: int, block_size: int, compute_units: int,
-              chunk_keys: int = 0) -> dict:
+              chunk_keys: int = 0, *, queries_per_kv: int) -> dict:
     """Host work plan from tv_tree_attention_plan (items/groups as int32 [n, 8])."""
     lib = _lib.library()
     count = len(prefix_lengths)
     prefixes = (ctypes.c_int32 * count)(*prefix_lengths)
     nodes = (ctypes.c_int32 * count)(*node_counts)
     info = _lib.PlanInfo()
-    _lib.check(lib.tv_tree_attention_plan(prefixes, nodes, count, num_kv_heads, block_size, compute_units,
-                                          chunk_keys, None, None, ctypes.byref(info)), "tree_attention_plan")
+    _lib.check(lib.tv_tree_attention_plan(prefixes, nodes, count, num_kv_heads, queries_per_kv, block_size,
+                                          compute_units, chunk_keys, None, None, ctypes.byref(info)),
+               "tree_attention_plan")
     items = np.zeros((max(info.num_items, 1), 8), dtype=np.int32)
     groups = np.zeros((max(info.num_groups, 1), 8), dtype=np.int32)
     _lib.check(lib.tv_tree_attention_plan(
-        prefixes, nodes, count, num_kv_heads, block_size, compute_units, chunk_keys,
+        prefixes, nodes, count, num_kv_heads, queries_per_kv, block_size, compute_units, chunk_keys,
         items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
         ctypes.byref(info)), "tree_attention_plan")
     return {"items": items[:info.num_items], "groups": groups[:info.num_groups],
@@ -181,7 +186,7 @@ def make_plan(prefix_lengths, node_counts, num_kv_heads: int, block_size: int, c
             "num_partial_slots": info.num_partial_slots, "workspace_bytes": int(info.workspace_bytes)}
 
 
-def fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads: int, status) -> None:
+def fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads: int, queries_per_kv: int, status) -> None:
     """The metadata, K/V pool and geometry fields of a tv_tree_attention_args block."""
     a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
     for i in range(4):
@@ -197,28 +202,29 @@ def fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads: int, status) -> No
     a.tree_slots = metadata.tree_slots.data_ptr()
     a.num_requests = metadata.num_requests
     a.total_queries = metadata.total_queries
-    a.num_q_heads = 4 * num_kv_heads
+    a.num_q_heads = queries_per_kv * num_kv_heads
     a.num_kv_heads = num_kv_heads
     a.head_dim = int(k_pool.shape[3])
     a.block_size = metadata.block_size
     a.status = status.data_ptr()
 
 
-def _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads: int, chunk_keys: int, stream: int):
+def _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads: int, queries_per_kv: int, chunk_keys: int,
+                    stream: int):
     """Filled argument block of one (metadata, K/V pool, stream): everything but Q, O and scale."""
-    state = derived_state(metadata, num_kv_heads, chunk_keys=chunk_keys)
+    state = derived_state(metadata, num_kv_heads, queries_per_kv=queries_per_kv, chunk_keys=chunk_keys)
     device = k_pool.device
     workspace = None
     if state["workspace_bytes"]:
         # One workspace per plan and stream: launches on one stream run in order, so the
         # per-layer launches of a round reuse it (each merge finishes before the next
         # layer's attention writes its partials).
-        ws_key = ("workspace", num_kv_heads, chunk_keys, stream)
+        ws_key = ("workspace", num_kv_heads, queries_per_kv, chunk_keys, stream)
         workspace = per_meta.get(ws_key)
         if workspace is None:
             workspace = per_meta[ws_key] = torch.empty(state["workspace_bytes"], dtype=torch.uint8, device=device)
     a = _lib.TreeAttentionArgs()
-    fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads, _device.status_word(device))
+    fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads, queries_per_kv, _device.status_word(device))
     a.ancestor_words = state["ancestor_words"].data_ptr()
     a.ancestor_words_per_row = state["words_per_row"]
     a.items = state["items_dev"].data_ptr()
@@ -244,16 +250,17 @@ def _capture_id(stream: int) -> int:
     return int(ident.value)
 
 
-def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int, chunk_keys: int,
-                     stream: int, exact: bool) -> torch.Tensor:
+def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int, queries_per_kv: int,
+                     chunk_keys: int, stream: int, exact: bool) -> torch.Tensor:
     """Graph-capturable launch that follows the live device metadata on every replay."""
     from .target_graph import GraphedTreeAttention
 
     per_meta = _per_metadata(metadata)
-    key = ("graph", num_kv_heads, chunk_keys)
+    key = ("graph", num_kv_heads, queries_per_kv, chunk_keys)
     graphed = per_meta.get(key)
     if graphed is None:
-        graphed = per_meta[key] = GraphedTreeAttention.for_signature(metadata, num_kv_heads, chunk_keys=chunk_keys)
+        graphed = per_meta[key] = GraphedTreeAttention.for_signature(
+            metadata, num_kv_heads, queries_per_kv=queries_per_kv, chunk_keys=chunk_keys)
     capture = _capture_id(stream)
     if graphed.prepared_capture != capture:
         graphed.prepare(metadata)   # recorded once at the head of this graph's sequence
@@ -268,17 +275,20 @@ def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0, exa
     if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
         q = q.contiguous()
     num_kv_heads = int(k_pool.shape[2])
+    queries_per_kv = int(q.shape[1]) // num_kv_heads
     stream = torch.cuda.current_stream(q.device).cuda_stream
     if torch.cuda.is_current_stream_capturing():
-        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, chunk_keys, stream, exact)
+        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, queries_per_kv, chunk_keys,
+                                stream, exact)
     per_meta = _derived.get(id(metadata))
     if per_meta is None:
         per_meta = _per_metadata(metadata)
-    key = (num_kv_heads, chunk_keys, k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(), v_pool.stride(),
-           k_pool.shape[0], k_pool.dtype, stream)
+    key = (num_kv_heads, queries_per_kv, chunk_keys, k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(),
+           v_pool.stride(), k_pool.shape[0], k_pool.dtype, stream)
     entry = per_meta.get(key)
     if entry is None:
-        entry = per_meta[key] = _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads, chunk_keys, stream)
+        entry = per_meta[key] = _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads, queries_per_kv,
+                                                chunk_keys, stream)
     a = _lib.TreeAttentionArgs.from_buffer_copy(entry[0])
     a.q = q.data_ptr()
     a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
@@ -361,8 +371,9 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
         raise ValueError("unsupported packed query/KV head geometry")
     if q.dtype not in (torch.bfloat16, torch.float16) or k_pool.dtype != q.dtype or v_pool.dtype != q.dtype:
         raise ValueError("the MI355X tree-attention kernel takes bf16 or f16 operands (FP32 Q/K/V unsupported)")
-    if num_queries_per_kv != 4 or head_size != 128:
-        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 4 query heads per KV head")
+    if num_queries_per_kv not in SUPPORTED_GROUPS or head_size != 128:
+        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 1, 2, 4, 8 or 16 "
+                         "query heads per KV head")
     if logical_kv_slots.dtype not in (torch.int32, torch.int64):
         raise ValueError("logical KV slots must be int32 or int64")
     if qq_bias.ndim != 2 or qq_bias.shape[0] < total_q or qq_bias.shape[1] < total_q:
@@ -404,12 +415,12 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     prefixes_host = (ctypes.c_int32 * 1)(prefix)
     nodes_host = (ctypes.c_int32 * 1)(total_q)
     cus = _device.compute_units(device.index if device.index is not None else torch.cuda.current_device())
-    _lib.check(lib.tv_tree_attention_plan_slots(prefixes_host, nodes_host, 1, num_kv_heads, cus, 0, None, None,
-                                                ctypes.byref(info)), "tree_attention_plan_slots")
+    _lib.check(lib.tv_tree_attention_plan_slots(prefixes_host, nodes_host, 1, num_kv_heads, num_queries_per_kv, cus,
+                                                0, None, None, ctypes.byref(info)), "tree_attention_plan_slots")
     items = np.zeros((max(info.num_items, 1), 8), dtype=np.int32)
     groups = np.zeros((max(info.num_groups, 1), 8), dtype=np.int32)
     _lib.check(lib.tv_tree_attention_plan_slots(
-        prefixes_host, nodes_host, 1, num_kv_heads, cus, 0, items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+        prefixes_host, nodes_host, 1, num_kv_heads, num_queries_per_kv, cus, 0, items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
         groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(info)), "tree_attention_plan_slots")
     items_dev = torch.from_numpy(items).to(device)
     groups_dev = torch.from_numpy(groups).to(device)

@@ -60,7 +60,7 @@ def ancestor_mask(parents: list[int]) -> np.ndarray:
 @dataclass
 class VerifyBatch:
     """One layer's packed verify inputs."""
-    q: torch.Tensor                 # [Q, 32, 128]
+    q: torch.Tensor                 # [Q, groups * KV heads, 128]
     k_pool: torch.Tensor            # [N, 256, 8, 128]
     v_pool: torch.Tensor
     metadata: PackedTreeMetadata
@@ -107,13 +107,15 @@ class VerifyBatch:
 
 def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: torch.device | str,
                        seed: int, dtype: torch.dtype = torch.bfloat16, pool_fill: float = 1.0,
-                       poison: bool = True, name: str = "", kv_heads: int = KV_HEADS) -> VerifyBatch:
+                       poison: bool = True, name: str = "", kv_heads: int = KV_HEADS,
+                       groups: int = Q_HEADS // KV_HEADS) -> VerifyBatch:
     """Pages and slots from a permuted pool; payloads N(0,1); unused rows NaN if `poison`.
 
     `pool_fill` < 1 sizes the pool so live pages fill that fraction (fragmentation).
     Tree K/V are written into their scratch slots (the post-append state) and also
     returned as `new_k`/`new_v` for timing the append.  `kv_heads` < 8 builds one
-    tensor-parallel shard: that many KV heads and 4 query heads per KV head.
+    tensor-parallel shard: that many KV heads.  `groups` is the number of query heads
+    per KV head (4 in the Qwen3-8B geometry).
     """
     device = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -140,7 +142,6 @@ def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: t
         offset += n
     metadata = PackedTreeMetadata.build(prefixes, tables, slots, masks, BLOCK)
     gen = torch.Generator(device=device).manual_seed(seed)
-    groups = Q_HEADS // KV_HEADS
     shape = (total_pages, BLOCK, kv_heads, HEAD_DIM)
     k_pool = torch.empty(shape, dtype=dtype, device=device)
     v_pool = torch.empty(shape, dtype=dtype, device=device)
@@ -164,7 +165,7 @@ def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: t
     k_pool.view(-1, kv_heads, HEAD_DIM)[tree_slots] = new_k
     v_pool.view(-1, kv_heads, HEAD_DIM)[tree_slots] = new_v
     return VerifyBatch(q=q, k_pool=k_pool, v_pool=v_pool, metadata=metadata, new_k=new_k, new_v=new_v,
-                       parents=[list(p) for p in trees], prefix_pages=tables, name=name,
+                       parents=[list(p) for p in trees], prefix_pages=tables, name=name, groups=groups,
                        info={"pages": total_pages, "pool_fill": pool_fill, "seed": seed})
 
 

@@ -29,9 +29,10 @@ def heap_parents(n):
 
 
 def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dtype=torch.bfloat16, seed=317,
-                      block=256):
+                      block=256, groups=4):
     """The reference GPU fixture geometry (tests/test_jetspec_packed_attention.py:109-125) with
-    shuffled pages, scattered scratch slots and NaN in every unused pool row."""
+    shuffled pages, scattered scratch slots and NaN in every unused pool row; `groups`
+    query heads per KV head."""
     rng = np.random.default_rng(seed)
     prefix_pages = [-(-p // block) for p in prefixes]
     scratch_pages = -(-sum(counts) // block) + 1
@@ -58,7 +59,7 @@ def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dt
     live = torch.cat(live + slots)
     k.view(-1, kv_heads, 128)[live] = torch.randn((live.numel(), kv_heads, 128), generator=gen, device=DEV).to(dtype)
     v.view(-1, kv_heads, 128)[live] = torch.randn((live.numel(), kv_heads, 128), generator=gen, device=DEV).to(dtype)
-    q = torch.randn((meta.total_queries, kv_heads * 4, 128), generator=gen, device=DEV).to(dtype)
+    q = torch.randn((meta.total_queries, kv_heads * groups, 128), generator=gen, device=DEV).to(dtype)
     return q, k, v, meta, slots, masks, parents
 
 

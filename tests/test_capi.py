@@ -66,9 +66,12 @@ def test_entry_points_reject_bad_arguments_without_a_device():
     assert lib.tv_truncate_accepted(None, 9, None, None, None, 0, None, 0, None, None, None, 0, None, None, None,
                                     None, None, None) == _lib.TV_OK
     with pytest.raises(ValueError, match="block_size"):
-        make_plan([10], [4], 8, 48, 256)
+        make_plan([10], [4], 8, 48, 256, queries_per_kv=4)
     with pytest.raises(ValueError, match="no tree nodes"):
-        make_plan([10], [0], 8, 256, 256)
+        make_plan([10], [0], 8, 256, 256, queries_per_kv=4)
+    for bad_group in (0, 3, 6, 32):
+        with pytest.raises(ValueError, match="query heads per KV head"):
+            make_plan([10], [4], 8, 256, 256, queries_per_kv=bad_group)
 
 
 def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
@@ -99,21 +102,26 @@ def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
     assert b"at most 2^31 slots" in lib.tv_last_error()
 
 
-def heads_per_group(nodes, kv_heads):
-    h = 2 if nodes <= 32 else 1
+def nodes_per_item(hpw, groups):
+    """A work item is 8 waves x 32 score rows: (8 / hpw) * (32 / groups) nodes per KV head."""
+    return (8 // hpw) * (32 // groups)
+
+
+def heads_per_group(nodes, kv_heads, groups=4):
+    h = 2 if nodes <= nodes_per_item(2, groups) else 1
     while h > 1 and h > kv_heads:
         h //= 2
     return h
 
 
-def check_plan_covers(prefixes, counts, kv_heads, cus, chunk=0, block=256):
-    plan = make_plan(prefixes, counts, kv_heads, block, cus, chunk)
-    items, groups = plan["items"], plan["groups"]
+def check_plan_covers(prefixes, counts, kv_heads, cus, chunk=0, block=256, groups=4):
+    plan = make_plan(prefixes, counts, kv_heads, block, cus, chunk, queries_per_kv=groups)
+    items, merges = plan["items"], plan["groups"]
     covered = {}
     slots_seen = set()
     for r, h0, n0, kbeg, kend, flags, slot, hpw in items.tolist():
-        assert hpw == heads_per_group(counts[r], kv_heads)
-        assert h0 % hpw == 0 and n0 % (64 // hpw) == 0
+        assert hpw == heads_per_group(counts[r], kv_heads, groups)
+        assert h0 % hpw == 0 and n0 % nodes_per_item(hpw, groups) == 0
         assert 0 <= kbeg <= kend <= prefixes[r] and kbeg % 32 == 0
         key = (r, h0, n0)
         covered.setdefault(key, []).append((kbeg, kend, flags, slot))
@@ -121,8 +129,8 @@ def check_plan_covers(prefixes, counts, kv_heads, cus, chunk=0, block=256):
             assert slot not in slots_seen
             slots_seen.add(slot)
     for r, (p, t) in enumerate(zip(prefixes, counts)):
-        hpw = heads_per_group(t, kv_heads)
-        npw = 64 // hpw
+        hpw = heads_per_group(t, kv_heads, groups)
+        npw = nodes_per_item(hpw, groups)
         for h0 in range(0, kv_heads, hpw):
             for n0 in range(0, t, npw):
                 ranges = sorted(covered.pop((r, h0, n0)))
@@ -137,7 +145,7 @@ def check_plan_covers(prefixes, counts, kv_heads, cus, chunk=0, block=256):
                     assert ranges[0][3] == -1
     assert not covered
     assert plan["num_partial_slots"] == len(slots_seen)
-    for r, h0, n0, hpw, first, ns, _, _ in groups.tolist():
+    for r, h0, n0, hpw, first, ns, _, _ in merges.tolist():
         assert set(range(first, first + ns)) <= slots_seen
     check_order(items.tolist(), counts)
     return plan
@@ -217,6 +225,17 @@ def test_plan_covers_every_row_and_key_once(prefixes, counts, kv_heads, chunk):
     check_plan_covers(prefixes, counts, kv_heads, 256, chunk)
 
 
+@pytest.mark.parametrize("groups", [1, 2, 8, 16])
+@pytest.mark.parametrize("kv_heads", [1, 2, 8])
+def test_plan_covers_every_row_and_key_once_per_group_size(groups, kv_heads):
+    """Items of (8 / hpw) * (32 / G) nodes: 256 nodes at G = 1 down to 16 at G = 16, and
+    the two-head form for trees up to half that."""
+    prefixes = [0, 1, 63, 64, 65, 255, 256, 257, 4096, 300, 9000]
+    counts = [1, 2, 16, 17, 32, 33, 64, 65, 512, 129, 256]
+    for chunk in (0, 64):
+        check_plan_covers(prefixes, counts, kv_heads, 256, chunk, groups=groups)
+
+
 def test_plan_at_benchmark_shapes():
     rng = np.random.default_rng(4)
     prefixes = [int(x) for x in rng.integers(8192, 32769, size=64)]
@@ -241,7 +260,7 @@ def test_plan_keeps_blocks_sharing_kv_on_one_xcd():
         streams.setdefault((r, h0, kbeg), set()).add(index % 8)
     multi = [xcds for key, xcds in streams.items() if counts[key[0]] > 64]
     assert multi and all(len(x) == 1 for x in multi)
-    plain = make_plan([9000 + 37 * i for i in range(64)], [64] * 64, 8, 256, 256)
+    plain = make_plan([9000 + 37 * i for i in range(64)], [64] * 64, 8, 256, 256, queries_per_kv=4)
     lengths = [kend - kbeg for (_, _, _, kbeg, kend, _, _, _) in plain["items"].tolist()]
     assert lengths == sorted(lengths, reverse=True)
 
@@ -272,22 +291,22 @@ def test_plan_fills_its_rounds_of_work_items():
     # More than 4 rounds of items (or a forced chunk length) is left as first chunked.
     rng = np.random.default_rng(5)
     prefixes = [int(x) for x in rng.integers(0, 16385, size=16)] + [int(x) for x in rng.integers(2048, 8193, size=32)]
-    plan = make_plan(prefixes, [512] * 16 + [32] * 32, 8, 256, 256)
+    plan = make_plan(prefixes, [512] * 16 + [32] * 32, 8, 256, 256, queries_per_kv=4)
     assert plan["num_items"] == 1152 and plan["num_groups"] == 0
 
 
-def _capacity(lib, counts, kv_heads, block, cus, chunk, max_prefix):
+def _capacity(lib, counts, kv_heads, block, cus, chunk, max_prefix, groups=4):
     info = _lib.PlanInfo()
     arr = (ctypes.c_int32 * len(counts))(*counts)
-    _lib.check(lib.tv_tree_attention_plan_capacity(arr, len(counts), kv_heads, block, cus, chunk, max_prefix,
+    _lib.check(lib.tv_tree_attention_plan_capacity(arr, len(counts), kv_heads, groups, block, cus, chunk, max_prefix,
                                                    ctypes.byref(info)), "capacity")
     return info
 
 
-def _capacity_packed(lib, counts, kv_heads, block, cus, chunk, max_prefix):
+def _capacity_packed(lib, counts, kv_heads, block, cus, chunk, max_prefix, groups=4):
     info = _lib.PlanInfo()
     _lib.check(lib.tv_tree_attention_plan_capacity_packed(sum(counts), len(counts), sum(n * n for n in counts),
-                                                          kv_heads, block, cus, chunk, max_prefix,
+                                                          kv_heads, groups, block, cus, chunk, max_prefix,
                                                           ctypes.byref(info)), "capacity_packed")
     return info
 
@@ -303,31 +322,33 @@ def test_signature_capacity_covers_every_node_count_vector():
         count = int(rng.integers(1, 9))
         high = int(rng.choice([40, 130, 300, 1024]))
         vectors.append(tuple(int(x) for x in rng.integers(1, high + 1, size=count)))
+    cases = [(8, 0, 4), (1, 0, 4), (2, 0, 4), (8, 2048, 4), (8, 0, 1), (2, 0, 16), (1, 0, 8), (8, 2048, 2)]
     for counts in vectors:
-        for kv_heads, chunk in ((8, 0), (1, 0), (2, 0), (8, 2048)):
+        for kv_heads, chunk, groups in cases:
+            where = (counts, kv_heads, chunk, groups)
             try:
-                exact = _capacity(lib, counts, kv_heads, 256, 256, chunk, 20000)
+                exact = _capacity(lib, counts, kv_heads, 256, 256, chunk, 20000, groups)
             except ValueError:   # beyond the device planner: the signature bound must refuse too
                 with pytest.raises(ValueError):
-                    _capacity_packed(lib, counts, kv_heads, 256, 256, chunk, 20000)
+                    _capacity_packed(lib, counts, kv_heads, 256, 256, chunk, 20000, groups)
                 continue
             try:
-                packed = _capacity_packed(lib, counts, kv_heads, 256, 256, chunk, 20000)
+                packed = _capacity_packed(lib, counts, kv_heads, 256, 256, chunk, 20000, groups)
             except ValueError as error:   # the class bound may exceed the planner: a refusal, never a short plan
                 assert "exceed" in str(error)
                 continue
-            assert packed.num_items >= exact.num_items, (counts, kv_heads, chunk)
-            assert packed.num_groups >= exact.num_groups, (counts, kv_heads, chunk)
-            assert packed.num_partial_slots >= exact.num_partial_slots, (counts, kv_heads, chunk)
-            assert packed.ancestor_words_per_row >= exact.ancestor_words_per_row, (counts, kv_heads, chunk)
-            assert packed.workspace_bytes >= exact.workspace_bytes, (counts, kv_heads, chunk)
+            assert packed.num_items >= exact.num_items, where
+            assert packed.num_groups >= exact.num_groups, where
+            assert packed.num_partial_slots >= exact.num_partial_slots, where
+            assert packed.ancestor_words_per_row >= exact.ancestor_words_per_row, where
+            assert packed.workspace_bytes >= exact.workspace_bytes, where
     # (12, 60, 72) and (24, 36, 84) share a signature; so do (1, 5, 6) and (2, 3, 7).
     a = _capacity_packed(lib, (12, 60, 72), 8, 256, 256, 0, 8192)
     b = _capacity_packed(lib, (24, 36, 84), 8, 256, 256, 0, 8192)
     assert (a.num_items, a.num_groups, a.ancestor_words_per_row) == (b.num_items, b.num_groups,
                                                                       b.ancestor_words_per_row)
     info = _lib.PlanInfo()
-    assert lib.tv_tree_attention_plan_capacity_packed(2, 3, 0, 8, 256, 256, 0, 100, ctypes.byref(info)) \
+    assert lib.tv_tree_attention_plan_capacity_packed(2, 3, 0, 8, 4, 256, 256, 0, 100, ctypes.byref(info)) \
         == _lib.TV_ERR_INVALID   # fewer rows than requests
 
 

@@ -46,7 +46,7 @@ ROUNDS = [
 ]
 
 
-def round_inputs(seed, counts, prefixes):
+def round_inputs(seed, counts, prefixes, groups=4):
     rng = np.random.default_rng(seed)
     perm = rng.permutation(PAGES)
     cursor, tables, slots, masks, depths = 0, [], [], [], []
@@ -68,7 +68,7 @@ def round_inputs(seed, counts, prefixes):
     positions = torch.tensor([prefixes[r] + d for r, ds in enumerate(depths) for d in ds], device=DEV)
     g = torch.Generator(device=DEV).manual_seed(seed)
     rows = sum(counts)
-    q = torch.randn(LAYERS, rows, 32, 128, generator=g, device=DEV).to(torch.bfloat16)
+    q = torch.randn(LAYERS, rows, 8 * groups, 128, generator=g, device=DEV).to(torch.bfloat16)
     k = torch.randn(LAYERS, rows, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     v = torch.randn(LAYERS, rows, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     return meta, positions, q, k, v
@@ -101,7 +101,7 @@ def forward(kv_pool, cache, metadata, positions, q, k, v, backend):
         rq = rope_scatter_prevalidated(q[layer], k[layer], v[layer], positions, cache, kp, vp, metadata.tree_slots,
                                        torch.empty_like(q[layer]))
         rotated.append(rq)
-        outs.append(packed_tree_attention(rq, kp, vp, metadata, SCALE, 4, backend=backend))
+        outs.append(packed_tree_attention(rq, kp, vp, metadata, SCALE, q.shape[2] // kp.shape[2], backend=backend))
     return torch.stack(rotated), torch.stack(outs)
 
 
@@ -111,12 +111,12 @@ def rope_cache():
     return torch.cat((angles.cos(), angles.sin()), -1).unsqueeze(1)
 
 
-@pytest.mark.parametrize("backend", ["auto", "gqa"])
-def test_captured_dropin_follows_staged_metadata(backend):
+@pytest.mark.parametrize("backend,groups", [("auto", 4), ("gqa", 4), ("auto", 1), ("gqa", 16)])
+def test_captured_dropin_follows_staged_metadata(backend, groups):
     g = torch.Generator(device=DEV).manual_seed(21)
     pool = torch.randn(2, LAYERS, PAGES, 256, 8, 128, generator=g, device=DEV).to(torch.bfloat16)
     cache = rope_cache()
-    meta0, pos0, q0, k0, v0 = round_inputs(500, *ROUNDS[0])
+    meta0, pos0, q0, k0, v0 = round_inputs(500, *ROUNDS[0], groups=groups)
     staged = staged_from(meta0)
     inputs = {"positions": pos0.clone(), "q": q0.clone(), "k": k0.clone(), "v": v0.clone()}
     stream = torch.cuda.Stream()
@@ -131,8 +131,8 @@ def test_captured_dropin_follows_staged_metadata(backend):
         captured = forward(pool, cache, staged, inputs["positions"], inputs["q"], inputs["k"], inputs["v"], backend)
     torch.cuda.synchronize()
     for index, (counts, prefixes) in enumerate(ROUNDS):
-        meta, positions, q, k, v = (meta0, pos0, q0, k0, v0) if index == 0 else round_inputs(500 + index, counts,
-                                                                                             prefixes)
+        meta, positions, q, k, v = (meta0, pos0, q0, k0, v0) if index == 0 else round_inputs(
+            500 + index, counts, prefixes, groups=groups)
         reference_pool = pool.clone()
         expect_rotated, expect_out = forward(reference_pool, cache, meta, positions, q, k, v, backend)
         torch.cuda.synchronize()
@@ -141,7 +141,7 @@ def test_captured_dropin_follows_staged_metadata(backend):
             inputs[name].copy_(value)
         graph.replay()
         torch.cuda.synchronize()
-        print(f"[capture/{backend}] round {index}: nodes {counts} prefixes {prefixes}", flush=True)
+        print(f"[capture/{backend}/G{groups}] round {index}: nodes {counts} prefixes {prefixes}", flush=True)
         rotated, out = captured[0].clone(), captured[1].clone()
         assert torch.equal(rotated.view(torch.int16), expect_rotated.view(torch.int16)), f"round {index} rope"
         assert torch.equal(pool.view(torch.int16), reference_pool.view(torch.int16)), f"round {index} pool"
@@ -149,7 +149,7 @@ def test_captured_dropin_follows_staged_metadata(backend):
         for layer in range(LAYERS):
             expected = oracle_rows(rotated[layer], pool[0, layer], pool[1, layer], meta, SCALE,
                                    list(range(meta.num_requests)))
-            assert_within_gate(out[layer], expected, f"capture/{backend} round {index} layer {layer}")
+            assert_within_gate(out[layer], expected, f"capture/{backend}/G{groups} round {index} layer {layer}")
         assert read_and_clear_status(DEV) == 0
         torch.randn(1 << 20, device=DEV).sum().item()   # eager work between replays
 

@@ -27,21 +27,21 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def device_plan(meta, kv_heads=8, chunk_keys=0, max_prefix=None):
+def device_plan(meta, kv_heads=8, chunk_keys=0, max_prefix=None, queries_per_kv=4):
     lib = _lib.library()
     count = meta.num_requests
     nodes = (ctypes.c_int32 * count)(*meta.node_counts_host)
     info = _lib.PlanInfo()
     bound = max(meta.prefix_lengths) if max_prefix is None else max_prefix
     cus = _device.compute_units(torch.cuda.current_device())
-    _lib.check(lib.tv_tree_attention_plan_capacity(nodes, count, kv_heads, meta.block_size, cus, chunk_keys, bound,
-                                                   ctypes.byref(info)), "capacity")
+    _lib.check(lib.tv_tree_attention_plan_capacity(nodes, count, kv_heads, queries_per_kv, meta.block_size, cus,
+                                                   chunk_keys, bound, ctypes.byref(info)), "capacity")
     items = torch.full((info.num_items, 8), -7, dtype=torch.int32, device=DEV)
     groups = torch.full((max(info.num_groups, 1), 8), -7, dtype=torch.int32, device=DEV)
     counts = torch.full((4,), -7, dtype=torch.int32, device=DEV)
     _lib.check(lib.tv_tree_attention_plan_device(meta.prefix_lens.data_ptr(), meta.node_counts.data_ptr(), count,
-                                                 kv_heads, meta.block_size, cus, chunk_keys, info.num_items,
-                                                 info.num_groups, info.num_partial_slots, items.data_ptr(),
+                                                 kv_heads, queries_per_kv, meta.block_size, cus, chunk_keys,
+                                                 info.num_items, info.num_groups, info.num_partial_slots, items.data_ptr(),
                                                  groups.data_ptr(), counts.data_ptr(),
                                                  _device.stream_handle(items.device)), "plan_device")
     counts = counts.tolist()
@@ -92,7 +92,8 @@ def test_device_plan_equals_host_plan(chunk_keys):
     cus = _device.compute_units(torch.cuda.current_device())
     cases = [(name, meta, 8) for name, meta in batches()] + (list(shard_batches()) if chunk_keys == 0 else [])
     for name, meta, kv in cases:
-        host = make_plan(meta.prefix_lengths, meta.node_counts_host, kv, meta.block_size, cus, chunk_keys)
+        host = make_plan(meta.prefix_lengths, meta.node_counts_host, kv, meta.block_size, cus, chunk_keys,
+                         queries_per_kv=4)
         print(f"[plan] {name} chunk={chunk_keys} items={host['num_items']} groups={host['num_groups']}", flush=True)
         if host["num_items"] > 8192:
             # Beyond the device planner's LDS sort: refused up front, never overrun.
@@ -110,9 +111,9 @@ def test_capacity_overflow_writes_zero_counts():
     lib = _lib.library()
     items = torch.zeros((2, 8), dtype=torch.int32, device=DEV)
     counts = torch.full((4,), -7, dtype=torch.int32, device=DEV)
-    _lib.check(lib.tv_tree_attention_plan_device(meta.prefix_lens.data_ptr(), meta.node_counts.data_ptr(), 1, 8, 256,
-                                                 256, 64, 2, 0, 0, items.data_ptr(), None, counts.data_ptr(), None),
-               "plan_device")
+    _lib.check(lib.tv_tree_attention_plan_device(meta.prefix_lens.data_ptr(), meta.node_counts.data_ptr(), 1, 8, 4,
+                                                 256, 256, 64, 2, 0, 0, items.data_ptr(), None, counts.data_ptr(),
+                                                 None), "plan_device")
     assert counts.tolist() == [0, 0, 0, 1]
 
 

@@ -40,7 +40,7 @@ def legacy_call(q, k, v, prefix, table, slots, mask):
         q, k.view(-1, 16, k.shape[2], k.shape[3]), v.view(-1, 16, v.shape[2], v.shape[3]),
         torch.zeros((1, (total + 15) // 16), device=DEV, dtype=torch.int32),
         torch.tensor([0, q.shape[0]], device=DEV, dtype=torch.int32),
-        torch.tensor([total], device=DEV, dtype=torch.int32), bias, SCALE, 4, 16,
+        torch.tensor([total], device=DEV, dtype=torch.int32), bias, SCALE, q.shape[1] // k.shape[2], 16,
         logical.reshape(1, -1), torch.tensor([0], device=DEV, dtype=torch.int32),
         torch.tensor([total], device=DEV, dtype=torch.int32))
 

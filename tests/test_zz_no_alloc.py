@@ -23,9 +23,10 @@ DEV = "cuda"
 
 def argument_block(batch, out, workspace):
     meta = batch.metadata
-    state = derived_state(meta, int(batch.k_pool.shape[2]))
+    kv_heads = int(batch.k_pool.shape[2])
+    state = derived_state(meta, kv_heads, queries_per_kv=batch.groups)
     a = _lib.TreeAttentionArgs()
-    fill_pool_args(a, meta, batch.k_pool, batch.v_pool, int(batch.k_pool.shape[2]), _device.status_word(out.device))
+    fill_pool_args(a, meta, batch.k_pool, batch.v_pool, kv_heads, batch.groups, _device.status_word(out.device))
     a.q = batch.q.data_ptr()
     a.q_stride_row, a.q_stride_head = batch.q.stride(0), batch.q.stride(1)
     a.out = out.data_ptr()
