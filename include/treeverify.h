@@ -63,7 +63,9 @@ enum tv_status_bits {
     TV_STATUS_BAD_SLOT = 2,     /* a store/commit slot outside the pool */
     TV_STATUS_BAD_REQUEST = 4,  /* metadata row that names a nonexistent request */
     TV_STATUS_BAD_POSITION = 8, /* a RoPE position outside the cos/sin cache */
-    TV_STATUS_BAD_DEPTH = 16    /* an accepted path node off its canonical depth */
+    TV_STATUS_BAD_DEPTH = 16,   /* an accepted path node off its canonical depth */
+    TV_STATUS_BAD_BIAS = 32     /* a qq_bias entry other than 0 / -inf packed into visibility
+                                   bits (finite values need tv_tree_attention_fp32) */
 };
 
 /* ABI version of the loaded library (TV_ABI_VERSION at build time). */
@@ -345,7 +347,9 @@ int tv_stream_capture_info(void* stream, int32_t* capturing, uint64_t* capture_i
  * (qq_bias f32, 0 = visible / -inf = hidden, row-major [local_q * T + node] at
  * qq_bias_offsets[r]; packed_metadata.py:93-100) into one bit per (row, node):
  * words[q * words_per_row + w] bit b is set iff node m = 64w + b satisfies
- * m < T, m <= local_q and qq_bias[...] == 0.
+ * m < T, m <= local_q and qq_bias[...] == 0.  An entry with m <= local_q that is
+ * neither 0 nor -inf (the reference would add it to the score) sets
+ * TV_STATUS_BAD_BIAS: bits cannot carry it.
  */
 int tv_pack_ancestor_words(const float* qq_bias, const int64_t* qq_bias_offsets,
                            const int32_t* query_to_request, const int32_t* query_local_row,
@@ -448,6 +452,63 @@ typedef struct tv_tree_attention_args {
  * prefix_slots).  The plan must have been made for the same G.
  */
 int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
+
+/*
+ * FP32 tree attention for every geometry the reference accepts: the MI355X form of
+ * the reference's scalar FP32 kernel _packed_paged_tree_fp32 (paged_backend.py:116-213),
+ * which its dispatcher runs for every batch outside its fast kernel's geometry
+ * (paged_backend.py:288-306), and of the legacy slot-addressed kernel
+ * (paged_backend.py:20-113).  Replaces them where tv_tree_attention's MFMA kernel does
+ * not apply: f32 operands, head sizes other than 128 (1..512), any number of query heads
+ * per KV head, page sizes that are not multiples of 32, trees above 1024 nodes, and
+ * finite qq_bias values (added to the score, as the reference does).
+ *
+ * out[q, h, :] = sum_k p_k V[k, h/G, :] / sum_k p_k with p_k = exp(s_k - max s) and
+ * s_k = scale * q[q,h,:] . K[k, h/G, :] (+ qq_bias[bias_off[r] + local * T + j] for tree
+ * key j); key position pos of request r is visible iff pos <= P + local.  Arithmetic,
+ * probabilities and the online softmax are fp32.  No plan or workspace: one wave per
+ * (packed row, KV head), reading every metadata value from device memory, so the launch
+ * is graph-capturable as is.  Out-of-range pages or slots set TV_STATUS_BAD_PAGE and
+ * that key is skipped; a row naming a nonexistent request sets TV_STATUS_BAD_REQUEST.
+ */
+typedef struct tv_tree_attention_fp32_args {
+    /* q [Q, Hq, D], head dim contiguous */
+    const void* q;
+    int64_t q_stride_row, q_stride_head;
+    /* k/v pools [N, B, Hkv, D], any element strides */
+    const void* k_pool;
+    const void* v_pool;
+    int64_t k_stride[4];
+    int64_t v_stride[4];
+    int64_t num_blocks;
+    int32_t in_dtype;                    /* TV_F32, TV_BF16 or TV_F16 (q, k and v) */
+    /* out [Q, Hq, D], head dim contiguous */
+    void* out;
+    int64_t out_stride_row, out_stride_head;
+    int32_t out_dtype;                   /* TV_F32, TV_BF16 or TV_F16 */
+    /* PackedTreeMetadata device buffers (packed_metadata.py:17-26) */
+    const int32_t* cu_seqlens_q;         /* [R+1] */
+    const int32_t* query_to_request;     /* [Q] */
+    const int32_t* query_local_row;      /* [Q] */
+    const int32_t* prefix_lens;          /* [R] */
+    const int32_t* node_counts;          /* [R] */
+    const int32_t* block_tables;         /* [R, table_stride]; unused with prefix_slots */
+    int64_t block_table_stride;
+    const int64_t* tree_slots;           /* [Q] */
+    const float* qq_bias;                /* per request [T, T], added to tree-key scores */
+    const int64_t* qq_bias_offsets;      /* [R+1] */
+    /* optional slot addressing of the prefix (legacy form), as in tv_tree_attention_args */
+    const void* prefix_slots;
+    int64_t prefix_slots_stride;
+    int32_t prefix_slots_is_int64;
+    int32_t num_requests, total_queries, num_q_heads, num_kv_heads, head_dim, block_size;
+    float scale;
+    int32_t* status;                     /* optional */
+} tv_tree_attention_fp32_args;
+
+int tv_tree_attention_fp32(const tv_tree_attention_fp32_args* args, void* stream);
+/* sizeof(tv_tree_attention_fp32_args) as compiled, for binding layout checks. */
+int64_t tv_sizeof_tree_attention_fp32_args(void);
 
 /*
  * Allocation-free variant of tv_tree_attention.  No counterpart in the reference: it is

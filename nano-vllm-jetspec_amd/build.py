@@ -27,6 +27,7 @@ ARCH = "gfx950"
 GROUPS = (1, 2, 4, 8, 16)
 ATTENTION_GROUP_SOURCES = tuple(f"tv_attention_g{g}.hip" for g in GROUPS)
 SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", *ATTENTION_GROUP_SOURCES,
+           "tv_attention_fp32.hip",
            "tv_rope.hip", "tv_accept.hip", "tv_metadata.hip", "tv_plan_device.hip")
 
 # Packed-FP32 VALU instructions are kept out of the device code (they are not

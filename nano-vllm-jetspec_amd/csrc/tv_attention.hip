@@ -98,10 +98,19 @@ pack_ancestor_kernel(const float* __restrict__ bias, const int64_t* __restrict__
         const int tn = counts[r];
         if (i >= 0 && i < tn) {
             const float* row = bias + bias_off[r] + static_cast<int64_t>(i) * tn;
+            bool other = false;   // a value bits cannot carry
             for (int b = 0; b < 64; ++b) {
                 const int m = 64 * w + b;
-                if (m < tn && m <= i && row[m] == 0.f) word |= 1ull << b;
+                if (m < tn && m <= i) {
+                    const float x = row[m];
+                    if (x == 0.f) {
+                        word |= 1ull << b;
+                    } else if (x != -INFINITY) {
+                        other = true;
+                    }
+                }
             }
+            if (other) set_status(status, TV_STATUS_BAD_BIAS);
         } else {
             set_status(status, TV_STATUS_BAD_REQUEST);
         }

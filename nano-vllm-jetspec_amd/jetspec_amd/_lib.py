@@ -29,6 +29,7 @@ TV_STATUS_BAD_SLOT = 2
 TV_STATUS_BAD_REQUEST = 4
 TV_STATUS_BAD_POSITION = 8
 TV_STATUS_BAD_DEPTH = 16
+TV_STATUS_BAD_BIAS = 32
 
 # Every extern "C" symbol of include/treeverify.h.
 EXPORTED_SYMBOLS = (
@@ -56,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "tv_stream_capture_info",
     "tv_tree_attention_noalloc",
     "tv_tree_attention_noalloc_max_workspace",
+    "tv_tree_attention_fp32",
+    "tv_sizeof_tree_attention_fp32_args",
 )
 
 
@@ -112,6 +115,45 @@ class TreeAttentionArgs(ctypes.Structure):
         ("prefix_slots_stride", c_int64),
         ("prefix_slots_is_int64", c_int32),
         ("exact_probabilities", c_int32),
+    ]
+
+
+class TreeAttentionFp32Args(ctypes.Structure):
+    _fields_ = [
+        ("q", c_void_p),
+        ("q_stride_row", c_int64),
+        ("q_stride_head", c_int64),
+        ("k_pool", c_void_p),
+        ("v_pool", c_void_p),
+        ("k_stride", c_int64 * 4),
+        ("v_stride", c_int64 * 4),
+        ("num_blocks", c_int64),
+        ("in_dtype", c_int32),
+        ("out", c_void_p),
+        ("out_stride_row", c_int64),
+        ("out_stride_head", c_int64),
+        ("out_dtype", c_int32),
+        ("cu_seqlens_q", c_void_p),
+        ("query_to_request", c_void_p),
+        ("query_local_row", c_void_p),
+        ("prefix_lens", c_void_p),
+        ("node_counts", c_void_p),
+        ("block_tables", c_void_p),
+        ("block_table_stride", c_int64),
+        ("tree_slots", c_void_p),
+        ("qq_bias", c_void_p),
+        ("qq_bias_offsets", c_void_p),
+        ("prefix_slots", c_void_p),
+        ("prefix_slots_stride", c_int64),
+        ("prefix_slots_is_int64", c_int32),
+        ("num_requests", c_int32),
+        ("total_queries", c_int32),
+        ("num_q_heads", c_int32),
+        ("num_kv_heads", c_int32),
+        ("head_dim", c_int32),
+        ("block_size", c_int32),
+        ("scale", c_float),
+        ("status", c_void_p),
     ]
 
 
@@ -178,6 +220,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_tree_attention_noalloc.argtypes = [POINTER(TreeAttentionArgs), c_void_p]
     lib.tv_tree_attention_noalloc_max_workspace.restype = c_int64
     lib.tv_tree_attention_noalloc_max_workspace.argtypes = []
+    lib.tv_tree_attention_fp32.restype = c_int32
+    lib.tv_tree_attention_fp32.argtypes = [POINTER(TreeAttentionFp32Args), c_void_p]
+    lib.tv_sizeof_tree_attention_fp32_args.restype = c_int64
+    lib.tv_sizeof_tree_attention_fp32_args.argtypes = []
     lib.tv_sizeof_rope_scatter_args.restype = c_int64
     lib.tv_sizeof_rope_scatter_args.argtypes = []
     lib.tv_rope_scatter.restype = c_int32

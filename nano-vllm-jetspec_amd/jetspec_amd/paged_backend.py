@@ -1,15 +1,22 @@
 """Packed ragged tree-verify attention on MI355X (drop-in for paged_backend.py:240-306).
 
 Every public entry keeps the reference's signature, argument meaning and ValueError
-conditions, and runs ONE hand-written HIP kernel (libtreeverify: tv_tree_attention).
-The reference's numerical variants (frozen FP32 ``reference``, ``prefix``, grouped
-``gqa``) differ only in tiling and precision knobs; here they are one kernel with
-bf16/f16 MFMA products, fp32 accumulation and online softmax, in two probability
-modes: ``auto`` and ``gqa`` round each probability to the operand type for the P.V
-product (as the reference's gqa backend, tree_gqa.py:102-105); the explicit FP32
-entries (``reference``, ``prefix``, and their modules' other entries) keep it to about
-2^-17 relative (two MFMAs: its rounding and the rounding of the remainder) and sum it
-in fp32, the reference's "never BF16 probabilities" (paged_backend.py:248-256).
+conditions, and runs hand-written HIP kernels (libtreeverify).  The reference's
+numerical variants (frozen FP32 ``reference``, ``prefix``, grouped ``gqa``) differ only
+in tiling and precision knobs; here they are one MFMA kernel (tv_tree_attention) with
+bf16/f16 products, fp32 accumulation and online softmax, in two probability modes:
+``auto`` and ``gqa`` round each probability to the operand type for the P.V product
+(as the reference's gqa backend, tree_gqa.py:102-105); the explicit FP32 entries
+(``reference``, ``prefix``, and their modules' other entries) keep it to about 2^-17
+relative (two MFMAs: its rounding and the rounding of the remainder) and sum it in
+fp32, the reference's "never BF16 probabilities" (paged_backend.py:248-256).
+
+Batches outside the MFMA kernel's geometry (f32 operands, head sizes other than 128,
+query groups other than 1/2/4/8/16, page sizes that are not multiples of 32, trees
+above 1024 nodes, unaligned pools) run the FP32 kernel (tv_tree_attention_fp32), as the
+reference's dispatcher runs its scalar FP32 kernel outside its fast kernel's geometry
+(paged_backend.py:288-306).  It reads every metadata value from device memory, needs
+no plan, and is capturable as is.
 
 Two launch modes, chosen per call:
 
@@ -51,13 +58,13 @@ _BACKENDS = ("auto", "reference", "prefix", "gqa")
 # Query heads per KV head the kernel is built for (the reference's grouped kernel takes
 # powers of two up to 16, tree_gqa.py:124-126).
 SUPPORTED_GROUPS = (1, 2, 4, 8, 16)
+_FP32_ROUTE = "fp32"     # cache entries of batches that run the FP32 kernel
 _derived: dict[int, dict] = {}
 _derived_lock = threading.Lock()
 
 
 def _validate(q, k_pool, v_pool, metadata, groups, output_dtype) -> torch.dtype:
-    """Geometry/device/dtype checks of tree_attention.py:21-37, then the kernel's own
-    limits; returns the output dtype."""
+    """Geometry/device/dtype checks of tree_attention.py:21-37; returns the output dtype."""
     if q.ndim != 3 or q.shape[0] != metadata.total_queries:
         raise ValueError("packed queries do not match the metadata")
     if k_pool.ndim != 4 or k_pool.shape != v_pool.shape or k_pool.shape[1] != metadata.block_size:
@@ -75,14 +82,76 @@ def _validate(q, k_pool, v_pool, metadata, groups, output_dtype) -> torch.dtype:
     dtype = q.dtype if output_dtype is None else output_dtype
     if dtype not in (q.dtype, torch.float32):
         raise ValueError("output dtype must match input or be FP32 for qualification")
-    if q.dtype == torch.float32:
-        raise ValueError("the MI355X tree-attention kernel takes bf16 or f16 operands (FP32 Q/K/V unsupported)")
-    if groups not in SUPPORTED_GROUPS or q.shape[-1] != 128:
-        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 1, 2, 4, 8 or 16 "
-                         "query heads per KV head")
-    if metadata.block_size % 32:
-        raise ValueError("the MI355X tree-attention kernel needs a page size that is a multiple of 32")
+    if q.shape[-1] > 512:
+        raise ValueError("the MI355X tree-attention kernels take head sizes up to 512")
     return dtype
+
+
+def _aligned_rows(t: torch.Tensor) -> bool:
+    """16-byte aligned base and row/page/head strides (the MFMA kernel's 16-byte loads)."""
+    return t.data_ptr() % 16 == 0 and all(t.stride(i) % 8 == 0 for i in range(t.ndim - 1))
+
+
+def _mfma_geometry(q, k_pool, v_pool, metadata) -> bool:
+    """True when the MFMA kernel (tv_tree_attention) takes this batch; the others run the
+    FP32 kernel.  Mirrors the MFMA entry's limits (csrc/tv_attention.hip)."""
+    if q.dtype not in (torch.bfloat16, torch.float16) or q.shape[-1] != 128:
+        return False
+    kv_heads = int(k_pool.shape[2])
+    if q.shape[1] % kv_heads or q.shape[1] // kv_heads not in SUPPORTED_GROUPS:
+        return False
+    if metadata.block_size % 32 or max(metadata.node_counts_host, default=0) > 1024:
+        return False
+    if k_pool.stride(3) != 1 or v_pool.stride(3) != 1 or not _aligned_rows(k_pool) or not _aligned_rows(v_pool):
+        return False
+    # 32-bit page, head and 32-key-tile byte offsets.
+    return all(0 <= t.stride(0) * 2 < (1 << 32) and 0 <= t.stride(1) * 64 < (1 << 31)
+               and 0 <= t.stride(2) * 2 < (1 << 31) for t in (k_pool, v_pool)) and (
+        int(k_pool.shape[0]) * metadata.block_size < (1 << 31))
+
+
+def _fp32_template(metadata, k_pool, v_pool, queries_per_kv: int, device):
+    """Filled FP32-kernel argument block of one (metadata, K/V pool): all but Q, O and scale."""
+    a = _lib.TreeAttentionFp32Args()
+    a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
+    for i in range(4):
+        a.k_stride[i] = k_pool.stride(i)
+        a.v_stride[i] = v_pool.stride(i)
+    a.num_blocks = int(k_pool.shape[0])
+    a.in_dtype = _device.dtype_code(k_pool.dtype)
+    a.cu_seqlens_q = metadata.cu_seqlens_q.data_ptr()
+    a.query_to_request = metadata.query_to_request.data_ptr()
+    a.query_local_row = metadata.query_local_row.data_ptr()
+    a.prefix_lens = metadata.prefix_lens.data_ptr()
+    a.node_counts = metadata.node_counts.data_ptr()
+    a.block_tables = metadata.block_tables.data_ptr()
+    a.block_table_stride = metadata.block_tables.stride(0)
+    a.tree_slots = metadata.tree_slots.data_ptr()
+    a.qq_bias = metadata.qq_bias.data_ptr()
+    a.qq_bias_offsets = metadata.qq_bias_offsets.data_ptr()
+    a.num_requests = metadata.num_requests
+    a.total_queries = metadata.total_queries
+    a.num_kv_heads = int(k_pool.shape[2])
+    a.num_q_heads = queries_per_kv * a.num_kv_heads
+    a.head_dim = int(k_pool.shape[3])
+    a.block_size = metadata.block_size
+    a.status = _device.status_word(device).data_ptr()
+    return a
+
+
+def _launch_fp32(a, q, out, scale, stream: int) -> torch.Tensor:
+    """Complete a copy of an FP32-kernel argument block with Q, O and scale, and launch."""
+    a = _lib.TreeAttentionFp32Args.from_buffer_copy(a)
+    if q.stride(-1) != 1 or out.stride(-1) != 1:
+        raise ValueError("unsupported packed query/KV head geometry")
+    a.q = q.data_ptr()
+    a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
+    a.out = out.data_ptr()
+    a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
+    a.out_dtype = _device.dtype_code(out.dtype)
+    a.scale = float(scale)
+    _lib.check(_lib.library().tv_tree_attention_fp32(ctypes.byref(a), stream), "tree_attention_fp32")
+    return out
 
 
 _METADATA_LAYOUT = (
@@ -271,24 +340,32 @@ def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int,
 def _launch(q, k_pool, v_pool, metadata, scale, out, *, chunk_keys: int = 0, exact: bool = False) -> torch.Tensor:
     """Enqueue the attention of `metadata` into `out`.  exact=True keeps every probability
     to ~2^-17 relative in the P.V product (the reference's FP32 entries); otherwise it is
-    rounded to the operand type once (the reference's grouped bf16-P kernel)."""
-    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
-        q = q.contiguous()
+    rounded to the operand type once (the reference's grouped bf16-P kernel).  Batches
+    outside the MFMA kernel's geometry run the FP32 kernel (fp32 probabilities)."""
     num_kv_heads = int(k_pool.shape[2])
     queries_per_kv = int(q.shape[1]) // num_kv_heads
     stream = torch.cuda.current_stream(q.device).cuda_stream
-    if torch.cuda.is_current_stream_capturing():
-        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, queries_per_kv, chunk_keys,
-                                stream, exact)
     per_meta = _derived.get(id(metadata))
     if per_meta is None:
         per_meta = _per_metadata(metadata)
     key = (num_kv_heads, queries_per_kv, chunk_keys, k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(),
-           v_pool.stride(), k_pool.shape[0], k_pool.dtype, stream)
+           v_pool.stride(), tuple(k_pool.shape), k_pool.dtype, stream)
     entry = per_meta.get(key)
     if entry is None:
-        entry = per_meta[key] = _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads, queries_per_kv,
-                                                chunk_keys, stream)
+        if not _mfma_geometry(q, k_pool, v_pool, metadata):
+            entry = per_meta[key] = (_FP32_ROUTE, _fp32_template(metadata, k_pool, v_pool, queries_per_kv, q.device))
+        elif torch.cuda.is_current_stream_capturing():
+            entry = None
+        else:
+            entry = per_meta[key] = _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads,
+                                                    queries_per_kv, chunk_keys, stream)
+    if entry is not None and entry[0] is _FP32_ROUTE:
+        return _launch_fp32(entry[1], q, out, scale, stream)
+    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if torch.cuda.is_current_stream_capturing():
+        return _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads, queries_per_kv, chunk_keys,
+                                stream, exact)
     a = _lib.TreeAttentionArgs.from_buffer_copy(entry[0])
     a.q = q.data_ptr()
     a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
@@ -345,15 +422,18 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     (models/qwen3.py:270-302): one request whose keys are named by a logical slot vector,
     ``logical_kv_slots[0, pos]`` for pos < seq_len (the committed prefix, then the T tree
     nodes), over a pool viewed as ``block_size``-token pages (16 in the c1 path), and a
-    request-local ``qq_bias[T, T]`` of 0 / -inf.  A key at position pos is visible to tree
-    row i iff pos <= P + i and, for a tree key, its bias is 0 (paged_backend.py:82-91).
+    request-local ``qq_bias[T, T]``.  A key at position pos is visible to tree row i iff
+    pos <= P + i; a tree key's bias is added to its score (paged_backend.py:82-91).
 
-    Runs the HIP kernel in slot-addressed mode with FP32 probabilities (the legacy kernel
-    is the frozen FP32 one, paged_backend.py:20-113).  Like the reference, it reads the
-    sequence length from the device (one synchronisation).  Multi-request calls are
-    rejected exactly as in the reference; the block-table form without logical slots or
-    bias runs the external jetspec kernel in the reference (paged_backend.py:362-363),
-    which is not part of this build, and is rejected too.
+    With a 0 / -inf bias (what the reference's runners build) and the MFMA kernel's
+    geometry, the MFMA kernel runs in slot-addressed mode with FP32 probabilities (the
+    legacy kernel is the frozen FP32 one, paged_backend.py:20-113); anything else (finite
+    bias values, f32 operands, other head sizes or query groups, trees above 1024 nodes)
+    runs the FP32 kernel.  Like the reference, it reads the sequence length from the
+    device (one synchronisation).  Multi-request calls are rejected exactly as in the
+    reference; the block-table form without logical slots or bias runs the external
+    jetspec kernel in the reference (paged_backend.py:362-363), which is not part of
+    this build, and is rejected too.
     """
     num_seqs = int(seq_lens_k.shape[0])
     if num_seqs != 1:
@@ -367,13 +447,14 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     device = _device.require_gpu(q, k_pool, v_pool, logical_kv_slots, qq_bias, seq_lens_k,
                                  what="paged_tree_attention")
     if (q.stride(-1) != 1 or k_pool.shape[3] != head_size or int(k_pool.shape[1]) != int(block_size)
-            or isinstance(num_queries_per_kv, bool) or num_query_heads != k_pool.shape[2] * num_queries_per_kv):
+            or isinstance(num_queries_per_kv, bool) or num_queries_per_kv <= 0
+            or num_query_heads != k_pool.shape[2] * num_queries_per_kv):
         raise ValueError("unsupported packed query/KV head geometry")
-    if q.dtype not in (torch.bfloat16, torch.float16) or k_pool.dtype != q.dtype or v_pool.dtype != q.dtype:
-        raise ValueError("the MI355X tree-attention kernel takes bf16 or f16 operands (FP32 Q/K/V unsupported)")
-    if num_queries_per_kv not in SUPPORTED_GROUPS or head_size != 128:
-        raise ValueError("the MI355X tree-attention kernel implements head_dim 128 with 1, 2, 4, 8 or 16 "
-                         "query heads per KV head")
+    if (q.dtype not in (torch.bfloat16, torch.float16, torch.float32) or k_pool.dtype != q.dtype
+            or v_pool.dtype != q.dtype):
+        raise ValueError("packed Q/K/V must use one supported floating dtype")
+    if head_size > 512:
+        raise ValueError("the MI355X tree-attention kernels take head sizes up to 512")
     if logical_kv_slots.dtype not in (torch.int32, torch.int64):
         raise ValueError("logical KV slots must be int32 or int64")
     if qq_bias.ndim != 2 or qq_bias.shape[0] < total_q or qq_bias.shape[1] < total_q:
@@ -383,33 +464,87 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     slots = logical_kv_slots.reshape(-1)
     if prefix < 0 or slots.numel() < seq_len or total_q < 1:
         raise ValueError("logical KV slots must cover the prefix and every tree node")
-    if total_q > 1024:
-        raise ValueError("the MI355X tree-attention kernel takes at most 1024 tree nodes per request")
     if not slots.is_contiguous():
         slots = slots.contiguous()
     bias = torch.as_strided(qq_bias, (total_q, total_q), (qq_bias.stride(0), qq_bias.stride(1))).to(
         torch.float32).contiguous().view(-1)
-    # The kernel reads the tree visibility as bits: a bias other than 0 / -inf (which the
-    # reference would add to the score) cannot be represented and is refused.
-    if not bool(((bias == 0) | (bias == float("-inf"))).all()):
-        raise ValueError("qq_bias entries must be 0 (visible) or -inf (hidden)")
-    num_kv_heads = int(k_pool.shape[2])
-    lib = _lib.library()
     i32 = dict(dtype=torch.int32, device=device)
-    cu = torch.tensor([0, total_q], **i32)
-    counts = torch.tensor([total_q], **i32)
-    rows_local = torch.arange(total_q, **i32)
-    requests = torch.zeros(total_q, **i32)
-    bias_offsets = torch.tensor([0, total_q * total_q], dtype=torch.int64, device=device)
-    tree_slots = slots[prefix:prefix + total_q].to(torch.int64)
-    prefix_lens = torch.tensor([prefix], **i32)
-    table = torch.full((1, 1), -1, **i32)
+    request = _LegacyRequest(
+        cu=torch.tensor([0, total_q], **i32), counts=torch.tensor([total_q], **i32),
+        rows_local=torch.arange(total_q, **i32), requests=torch.zeros(total_q, **i32),
+        bias=bias, bias_offsets=torch.tensor([0, total_q * total_q], dtype=torch.int64, device=device),
+        tree_slots=slots[prefix:prefix + total_q].to(torch.int64), prefix_lens=torch.tensor([prefix], **i32),
+        table=torch.full((1, 1), -1, **i32), slots=slots, prefix=prefix, total_q=total_q)
+    out = torch.empty_like(q)
+    # The MFMA kernel reads tree visibility as bits, so a bias other than 0 / -inf (which
+    # is added to the score) takes the FP32 kernel.
+    mask_bias = bool(((bias == 0) | (bias == float("-inf"))).all())
+    geometry = (q.dtype != torch.float32 and head_size == 128 and num_queries_per_kv in SUPPORTED_GROUPS
+                and total_q <= 1024 and k_pool.stride(3) == 1 and v_pool.stride(3) == 1
+                and _aligned_rows(k_pool) and _aligned_rows(v_pool)
+                and int(k_pool.shape[0]) * int(block_size) < (1 << 31))
+    if mask_bias and geometry:
+        _legacy_mfma(q, k_pool, v_pool, request, scale, num_queries_per_kv, int(block_size), out, device)
+    else:
+        _legacy_fp32(q, k_pool, v_pool, request, scale, int(block_size), out, device)
+    return out
+
+
+class _LegacyRequest:
+    """Device metadata of the legacy entry's one request (kept alive until the launch returns)."""
+
+    def __init__(self, **fields):
+        self.__dict__.update(fields)
+
+
+def _legacy_fp32(q, k_pool, v_pool, req, scale, block_size: int, out, device) -> None:
+    a = _lib.TreeAttentionFp32Args()
+    a.q = q.data_ptr()
+    a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
+    a.k_pool, a.v_pool = k_pool.data_ptr(), v_pool.data_ptr()
+    for i in range(4):
+        a.k_stride[i] = k_pool.stride(i)
+        a.v_stride[i] = v_pool.stride(i)
+    a.num_blocks = int(k_pool.shape[0])
+    a.in_dtype = _device.dtype_code(q.dtype)
+    a.out = out.data_ptr()
+    a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
+    a.out_dtype = _device.dtype_code(out.dtype)
+    a.cu_seqlens_q = req.cu.data_ptr()
+    a.query_to_request = req.requests.data_ptr()
+    a.query_local_row = req.rows_local.data_ptr()
+    a.prefix_lens = req.prefix_lens.data_ptr()
+    a.node_counts = req.counts.data_ptr()
+    a.block_tables = req.table.data_ptr()
+    a.block_table_stride = 1
+    a.tree_slots = req.tree_slots.data_ptr()
+    a.qq_bias = req.bias.data_ptr()
+    a.qq_bias_offsets = req.bias_offsets.data_ptr()
+    a.prefix_slots = req.slots.data_ptr()
+    a.prefix_slots_stride = 0
+    a.prefix_slots_is_int64 = 1 if req.slots.dtype == torch.int64 else 0
+    a.num_requests = 1
+    a.total_queries = req.total_q
+    a.num_q_heads = int(q.shape[1])
+    a.num_kv_heads = int(k_pool.shape[2])
+    a.head_dim = int(q.shape[2])
+    a.block_size = block_size
+    a.scale = float(scale)
+    a.status = _device.status_word(device).data_ptr()
+    _lib.check(_lib.library().tv_tree_attention_fp32(ctypes.byref(a), _device.stream_handle(device)),
+               "tree_attention_fp32 (slot addressed)")
+
+
+def _legacy_mfma(q, k_pool, v_pool, req, scale, num_queries_per_kv: int, block_size: int, out, device) -> None:
+    lib = _lib.library()
+    total_q, prefix = req.total_q, req.prefix
+    num_kv_heads = int(k_pool.shape[2])
     stream = _device.stream_handle(device)
     status = _device.status_word(device)
     per_row = (total_q + 63) // 64
     words = torch.empty((total_q, per_row), dtype=torch.int64, device=device)
-    _lib.check(lib.tv_pack_ancestor_words(bias.data_ptr(), bias_offsets.data_ptr(), requests.data_ptr(),
-                                          rows_local.data_ptr(), counts.data_ptr(), total_q, 1, per_row,
+    _lib.check(lib.tv_pack_ancestor_words(req.bias.data_ptr(), req.bias_offsets.data_ptr(), req.requests.data_ptr(),
+                                          req.rows_local.data_ptr(), req.counts.data_ptr(), total_q, 1, per_row,
                                           words.data_ptr(), status.data_ptr(), stream), "pack_ancestor_words")
     info = _lib.PlanInfo()
     prefixes_host = (ctypes.c_int32 * 1)(prefix)
@@ -420,14 +555,14 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     items = np.zeros((max(info.num_items, 1), 8), dtype=np.int32)
     groups = np.zeros((max(info.num_groups, 1), 8), dtype=np.int32)
     _lib.check(lib.tv_tree_attention_plan_slots(
-        prefixes_host, nodes_host, 1, num_kv_heads, num_queries_per_kv, cus, 0, items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
-        groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), ctypes.byref(info)), "tree_attention_plan_slots")
+        prefixes_host, nodes_host, 1, num_kv_heads, num_queries_per_kv, cus, 0,
+        items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+        ctypes.byref(info)), "tree_attention_plan_slots")
     items_dev = torch.from_numpy(items).to(device)
     groups_dev = torch.from_numpy(groups).to(device)
     workspace = torch.empty(max(int(info.workspace_bytes), 1), dtype=torch.uint8, device=device)
     if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
         q = q.contiguous()
-    out = torch.empty_like(q)
     a = _lib.TreeAttentionArgs()
     a.q = q.data_ptr()
     a.q_stride_row, a.q_stride_head = q.stride(0), q.stride(1)
@@ -440,20 +575,20 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     a.out = out.data_ptr()
     a.out_stride_row, a.out_stride_head = out.stride(0), out.stride(1)
     a.out_dtype = _device.dtype_code(out.dtype)
-    a.cu_seqlens_q = cu.data_ptr()
-    a.prefix_lens = prefix_lens.data_ptr()
-    a.node_counts = counts.data_ptr()
-    a.block_tables = table.data_ptr()
+    a.cu_seqlens_q = req.cu.data_ptr()
+    a.prefix_lens = req.prefix_lens.data_ptr()
+    a.node_counts = req.counts.data_ptr()
+    a.block_tables = req.table.data_ptr()
     a.block_table_stride = 1
-    a.tree_slots = tree_slots.data_ptr()
+    a.tree_slots = req.tree_slots.data_ptr()
     a.ancestor_words = words.data_ptr()
     a.ancestor_words_per_row = per_row
     a.num_requests = 1
     a.total_queries = total_q
-    a.num_q_heads = num_query_heads
+    a.num_q_heads = int(q.shape[1])
     a.num_kv_heads = num_kv_heads
-    a.head_dim = head_size
-    a.block_size = int(block_size)
+    a.head_dim = int(q.shape[2])
+    a.block_size = block_size
     a.scale = float(scale)
     a.items = items_dev.data_ptr()
     a.num_items = info.num_items
@@ -463,9 +598,8 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     a.workspace = workspace.data_ptr() if info.workspace_bytes else None
     a.workspace_bytes = int(info.workspace_bytes)
     a.status = status.data_ptr()
-    a.prefix_slots = slots.data_ptr()
+    a.prefix_slots = req.slots.data_ptr()
     a.prefix_slots_stride = 0
-    a.prefix_slots_is_int64 = 1 if slots.dtype == torch.int64 else 0
+    a.prefix_slots_is_int64 = 1 if req.slots.dtype == torch.int64 else 0
     a.exact_probabilities = 1
     _lib.check(lib.tv_tree_attention(ctypes.byref(a), stream), "tree_attention (slot addressed)")
-    return out

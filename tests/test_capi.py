@@ -37,6 +37,7 @@ def test_abi_version_and_struct_layout():
     lib = _lib.library()
     assert lib.tv_abi_version() == _lib.ABI_VERSION
     assert lib.tv_sizeof_tree_attention_args() == ctypes.sizeof(_lib.TreeAttentionArgs)
+    assert lib.tv_sizeof_tree_attention_fp32_args() == ctypes.sizeof(_lib.TreeAttentionFp32Args)
     assert lib.tv_last_error() is not None
 
 
@@ -72,6 +73,41 @@ def test_entry_points_reject_bad_arguments_without_a_device():
     for bad_group in (0, 3, 6, 32):
         with pytest.raises(ValueError, match="query heads per KV head"):
             make_plan([10], [4], 8, 256, 256, queries_per_kv=bad_group)
+
+
+def test_fp32_attention_rejects_bad_arguments_without_a_device():
+    lib = _lib.library()
+    assert lib.tv_tree_attention_fp32(None, None) == _lib.TV_ERR_INVALID
+
+    def args(**over):
+        a = _lib.TreeAttentionFp32Args()
+        a.q = a.k_pool = a.v_pool = a.out = 0x10000
+        a.cu_seqlens_q = a.query_to_request = a.query_local_row = a.prefix_lens = a.node_counts = 0x10000
+        a.block_tables = a.tree_slots = a.qq_bias = a.qq_bias_offsets = 0x10000
+        a.in_dtype = a.out_dtype = _lib.TV_F32
+        a.num_requests, a.total_queries = 1, 4
+        a.num_q_heads, a.num_kv_heads, a.head_dim, a.block_size = 6, 2, 96, 16
+        a.num_blocks = 8
+        a.scale = 0.1
+        for name, value in over.items():
+            setattr(a, name, value)
+        return a
+    cases = [
+        (dict(num_q_heads=5), _lib.TV_ERR_INVALID, b"query heads over"),
+        (dict(num_kv_heads=0), _lib.TV_ERR_INVALID, b"query heads over"),
+        (dict(head_dim=513), _lib.TV_ERR_UNSUPPORTED, b"head_dim 513"),
+        (dict(head_dim=0), _lib.TV_ERR_UNSUPPORTED, b"head_dim 0"),
+        (dict(block_size=0), _lib.TV_ERR_INVALID, b"pool geometry"),
+        (dict(in_dtype=7), _lib.TV_ERR_INVALID, b"dtypes"),
+        (dict(scale=float("nan")), _lib.TV_ERR_INVALID, b"finite"),
+        (dict(qq_bias=None), _lib.TV_ERR_INVALID, b"null pointer"),
+        (dict(num_requests=0), _lib.TV_ERR_INVALID, b"counts"),
+    ]
+    for over, code, message in cases:
+        assert lib.tv_tree_attention_fp32(ctypes.byref(args(**over)), None) == code, over
+        assert message in lib.tv_last_error(), (over, lib.tv_last_error())
+    # No rows: nothing to launch (no device needed).
+    assert lib.tv_tree_attention_fp32(ctypes.byref(args(total_queries=0)), None) == _lib.TV_OK
 
 
 def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():

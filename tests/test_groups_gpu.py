@@ -29,7 +29,7 @@ from gpu_helpers import assert_within_gate, metrics, oracle_rows
 from jetspec_amd import (PackedTreeMetadata, packed_tree_attention, packed_tree_attention_reference,
                          read_and_clear_status)
 from jetspec_amd import _device
-from jetspec_amd.paged_backend import _launch, make_plan
+from jetspec_amd.paged_backend import _launch, _mfma_geometry, make_plan
 from jetspec_amd.target_graph import GraphedTreeAttention
 from test_attention_gpu import reference_fixture
 from test_graph_gpu import device_plan
@@ -148,9 +148,17 @@ def test_legacy_entry_equals_packed_fp32_entry(groups):
     assert read_and_clear_status(DEV) == 0
 
 
-def test_unsupported_group_sizes_are_refused():
+def test_other_group_sizes_take_the_fp32_kernel():
+    """Group sizes outside {1, 2, 4, 8, 16} run the FP32 kernel (tests/test_fp32_kernel_gpu.py
+    checks its values); the grouped entry refuses them as the reference's does."""
     q, k, v, meta, *_ = reference_fixture(kv_heads=1, groups=4)
+    assert _mfma_geometry(q, k, v, meta)
     for heads in (3, 6, 32):
-        bad_q = torch.zeros((q.shape[0], heads, 128), dtype=q.dtype, device=DEV)
-        with pytest.raises(ValueError, match="query heads per KV head"):
-            packed_tree_attention(bad_q, k, v, meta, SCALE, heads)
+        other = torch.randn((q.shape[0], heads, 128), device=DEV).to(q.dtype)
+        assert not _mfma_geometry(other, k, v, meta)
+        out = packed_tree_attention(other, k, v, meta, SCALE, heads)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out.float()).all().item()
+        with pytest.raises(ValueError, match="power-of-two GQA"):
+            packed_tree_attention(other, k, v, meta, SCALE, heads, backend="gqa")
+    assert read_and_clear_status(DEV) == 0

@@ -73,13 +73,19 @@ def test_legacy_rejections():
         paged_tree_attention(local_q, k, v, None, None, torch.tensor([3, 4], device=DEV), None, SCALE, 4, 256)
     with pytest.raises(ValueError, match="external jetspec kernel"):
         paged_tree_attention(local_q, k, v, None, None, torch.tensor([3], device=DEV), None, SCALE, 4, 256)
+    # A finite bias is added to the score (paged_backend.py:82-91): it runs on the FP32
+    # kernel and moves only its own row (tests/test_fp32_kernel_gpu.py checks the values).
     bias = torch.where(masks[0], 0.0, float("-inf")).float()
-    bias[5, 0] = 0.5   # a finite nonzero bias cannot be expressed as visibility bits
+    bias[5, 0] = 0.5
     logical = torch.cat((torch.arange(65, device=DEV) + 256 * meta.block_tables_host[0][0], slots[0]))
-    with pytest.raises(ValueError, match="0 \\(visible\\) or -inf"):
-        paged_tree_attention(local_q, k.view(-1, 16, 2, 128), v.view(-1, 16, 2, 128), None, None,
-                             torch.tensor([65 + local_q.shape[0]], device=DEV), bias, SCALE, 4, 16,
-                             logical.view(1, -1))
+    biased = paged_tree_attention(local_q, k.view(-1, 16, 2, 128), v.view(-1, 16, 2, 128), None, None,
+                                  torch.tensor([65 + local_q.shape[0]], device=DEV), bias, SCALE, 4, 16,
+                                  logical.view(1, -1))
+    plain = legacy_call(local_q, k, v, 65, meta.block_tables_host[0], slots[0], masks[0])
+    diff = (biased.float() - plain.float()).abs().amax(dim=(1, 2))
+    assert diff[5].item() > 1e-3
+    assert torch.cat((diff[:5], diff[6:])).max().item() < 2e-2
+    assert read_and_clear_status(DEV) == 0
 
 
 @pytest.mark.parametrize("case", ["fixture", "config2", "forced_split", "config5_sampled"])
