@@ -253,8 +253,9 @@ int tv_truncate_accepted(const int32_t* paths, int32_t path_stride, const int32_
  * copies (PackedTreeMetadata.prefix_lengths / node_counts_host).
  * Call once with NULL outputs to learn the sizes (written to *info), then again
  * with buffers of at least info->num_items * 8 and info->num_groups * 8 int32.
- *   queries_per_kv: query heads per KV head, G (1, 2, 4, 8 or 16); a work item holds
- *               256 score rows = (8 / HPW) * (32 / G) nodes x G heads x HPW KV heads.
+ *   queries_per_kv: query heads per KV head, G (1 to 8, or 16); a work item holds
+ *               256 score rows = (8 / HPW) * floor(32 / G) nodes x G heads x HPW KV heads
+ *               (plus padding rows when G does not divide 32).
  *   num_compute_units: CUs of the target device (256 on MI355X).
  *   chunk_keys: 0 = automatic; > 0 forces every prefix chunk to that many keys
  *               (a multiple of 32), which makes per-request results independent
@@ -447,9 +448,10 @@ typedef struct tv_tree_attention_args {
  * fp32 accumulation and online softmax, probabilities rounded to the operand
  * type for the P.V product (tree_gqa.py:102-105).
  * Implemented geometry: head_dim 128, num_q_heads == G * num_kv_heads with G in
- * {1, 2, 4, 8, 16} (the reference's grouped kernel takes powers of two up to 16,
- * tree_gqa.py:124-126), block_size % 32 == 0 (any positive block_size with
- * prefix_slots).  The plan must have been made for the same G.
+ * 1..8 or 16 (the reference's grouped kernel takes powers of two up to 16,
+ * tree_gqa.py:124-126; its FP32 kernel any G, as tv_tree_attention_fp32 does),
+ * block_size % 32 == 0 (any positive block_size with prefix_slots).  The plan must
+ * have been made for the same G.
  */
 int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
 

@@ -24,7 +24,7 @@ OUTPUT = HERE / "jetspec_amd" / "libtreeverify.so"
 ARCH = "gfx950"
 
 # Query heads per KV head the attention kernel is instantiated for.
-GROUPS = (1, 2, 4, 8, 16)
+GROUPS = (1, 2, 3, 4, 5, 6, 7, 8, 16)
 ATTENTION_GROUP_SOURCES = tuple(f"tv_attention_g{g}.hip" for g in GROUPS)
 SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", *ATTENTION_GROUP_SOURCES,
            "tv_attention_fp32.hip",

@@ -54,7 +54,11 @@ struct AttnParams {
 // launch status with check_launch.
 int launch_tree_attention_g1(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_g2(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_g3(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_g4(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_g5(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_g6(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_g7(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_g8(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_g16(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 

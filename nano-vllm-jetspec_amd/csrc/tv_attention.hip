@@ -26,7 +26,7 @@ merge_partials_kernel(const AttnParams p) {
     const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
     if (r < 0 || r >= p.num_requests) return;
     const int wph = 8 / hpw;
-    const int G = p.qpk, nw = 32 / G;   // query heads per KV head, nodes per wave
+    const int G = p.qpk, nw = 32 / G;   // query heads per KV head, nodes per wave (floor)
     const int wr = 8 * blockIdx.y + (threadIdx.x >> 5), quad = threadIdx.x & 31;
     const int wave = wr >> 5, c = wr & 31;
     const int hl = wave / wph;
@@ -75,7 +75,7 @@ merge_partials_kernel(const AttnParams p) {
         }
         m = mb;
     }
-    if (head >= p.num_kv_heads || node >= tn) return;
+    if (head >= p.num_kv_heads || node >= tn || c >= nw * G) return;   // c >= nw * G: padding row
     const float inv = 1.f / l;
     store_out4<T>(p, qbase + node, qh, 4 * quad, o * inv);
 }
@@ -160,9 +160,9 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     }
     const int32_t qpk = a->num_kv_heads >= 1 && a->num_q_heads % a->num_kv_heads == 0
                             ? a->num_q_heads / a->num_kv_heads : 0;
-    if (qpk != 1 && qpk != 2 && qpk != 4 && qpk != 8 && qpk != 16) {
+    if (!((qpk >= 1 && qpk <= 8) || qpk == 16)) {
         return fail(TV_ERR_UNSUPPORTED,
-                    "tree_attention: %d query heads over %d KV heads (implemented: 1, 2, 4, 8 or 16 per KV head)",
+                    "tree_attention: %d query heads over %d KV heads (implemented: 1 to 8 or 16 per KV head)",
                     a->num_q_heads, a->num_kv_heads);
     }
     if (a->prefix_slots ? a->block_size < 1 : (a->block_size < 32 || a->block_size % 32)) {
@@ -278,7 +278,11 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     switch (qpk) {
         case 1: launch_tree_attention_g1(p, a->num_items, bf16, exact, s); break;
         case 2: launch_tree_attention_g2(p, a->num_items, bf16, exact, s); break;
+        case 3: launch_tree_attention_g3(p, a->num_items, bf16, exact, s); break;
         case 4: launch_tree_attention_g4(p, a->num_items, bf16, exact, s); break;
+        case 5: launch_tree_attention_g5(p, a->num_items, bf16, exact, s); break;
+        case 6: launch_tree_attention_g6(p, a->num_items, bf16, exact, s); break;
+        case 7: launch_tree_attention_g7(p, a->num_items, bf16, exact, s); break;
         case 8: launch_tree_attention_g8(p, a->num_items, bf16, exact, s); break;
         default: launch_tree_attention_g16(p, a->num_items, bf16, exact, s); break;
     }

@@ -47,8 +47,9 @@
 // values <= 1, so the result is the same online softmax with fewer rescales.
 //
 // This header holds the kernel templates; tv_attention_g<G>.hip instantiates them for one
-// group size G (query heads per KV head: 1, 2, 4, 8 or 16).  A wave's 32 score rows are
-// 32 / G nodes x G query heads of one KV head.
+// group size G (query heads per KV head: 1-8 or 16).  A wave's 32 score rows are
+// NW = floor(32 / G) nodes x G query heads of one KV head; when G does not divide 32 the
+// last 32 - NW * G rows are padding (zero Q, never stored).
 #pragma once
 
 #include "tv_attention.h"
@@ -163,6 +164,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     constexpr int WPH = 8 / HPW;                        // waves per KV head
     constexpr int NW = 32 / G;                          // nodes per wave (G query heads each)
     constexpr int NPW = NW * WPH;                       // nodes per workgroup
+    static_assert(G >= 1 && G <= 16, "query heads per KV head");
     // LDS ring of NS stages.  K tiles, V tiles and ancestor words live in three regions
     // so every operand address is a per-lane constant plus a compile-time stage offset.
     constexpr int NS = HPW == 1 ? 8 : 4;
@@ -185,7 +187,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const int qh = head * G + c % G;
     const bool head_ok = head < p.num_kv_heads;
     const bool wave_active = head_ok && (it.n0 + NW * nsub) < tn;
-    const bool row_ok = head_ok && node < tn;
+    // Rows past NW * G (G not dividing 32) are padding: they load no Q and store nothing.
+    const bool row_ok = head_ok && c < NW * G && node < tn;
     const int tree_end = (it.flags & 1) ? min(tn, it.n0 + NPW) : 0;
     const int ntp = (it.kend - it.kbeg + kTileKeys - 1) / kTileKeys;
     const int nt = ntp + (tree_end + kTileKeys - 1) / kTileKeys;

@@ -39,12 +39,13 @@ struct Item {
     int32_t hg, chunk, nb;
 };
 
-// A wave owns 32 score rows = 32 / qpk nodes x qpk query heads, so a workgroup of 8 waves
-// holds (8 / hpw) * (32 / qpk) nodes of each of its hpw KV heads; trees that fit the
-// two-head form (<= 32 nodes at qpk 4) take it.
+// A wave owns 32 score rows = floor(32 / qpk) nodes x qpk query heads (plus padding rows
+// when qpk does not divide 32), so a workgroup of 8 waves holds (8 / hpw) * floor(32 / qpk)
+// nodes of each of its hpw KV heads; trees that fit the two-head form (<= 32 nodes at
+// qpk 4) take it.
 int nodes_per_item(int hpw, int32_t qpk) { return (8 / hpw) * (32 / qpk); }
 
-bool supported_group(int32_t qpk) { return qpk == 1 || qpk == 2 || qpk == 4 || qpk == 8 || qpk == 16; }
+bool supported_group(int32_t qpk) { return (qpk >= 1 && qpk <= 8) || qpk == 16; }
 
 int heads_per_group(int32_t nodes, int32_t kv_heads, int32_t qpk) {
     int h = nodes <= nodes_per_item(2, qpk) ? 2 : 1;
@@ -161,7 +162,7 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
     if (num_requests < 1) return fail(TV_ERR_INVALID, "plan: at least one request is required");
     if (num_kv_heads < 1) return fail(TV_ERR_INVALID, "plan: num_kv_heads must be positive");
     if (!supported_group(qpk)) {
-        return fail(TV_ERR_UNSUPPORTED, "plan: %d query heads per KV head (implemented: 1, 2, 4, 8 or 16)", qpk);
+        return fail(TV_ERR_UNSUPPORTED, "plan: %d query heads per KV head (implemented: 1 to 8 or 16)", qpk);
     }
     if (num_compute_units < 1) return fail(TV_ERR_INVALID, "plan: num_compute_units must be positive");
     if (chunk_keys < 0 || chunk_keys % 32) {

@@ -464,7 +464,7 @@ int fill_capacity(int64_t blocks, int32_t max_nodes, int32_t block_size, int32_t
     return TV_OK;
 }
 
-bool supported_group(int32_t qpk) { return qpk == 1 || qpk == 2 || qpk == 4 || qpk == 8 || qpk == 16; }
+bool supported_group(int32_t qpk) { return (qpk >= 1 && qpk <= 8) || qpk == 16; }
 
 bool capacity_args_ok(int32_t num_requests, int32_t num_kv_heads, int32_t qpk, int32_t block_size,
                       int32_t num_compute_units, int32_t chunk_keys, int64_t max_prefix) {

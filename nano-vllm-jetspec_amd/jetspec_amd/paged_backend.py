@@ -55,9 +55,10 @@ import torch
 from . import _device, _lib
 
 _BACKENDS = ("auto", "reference", "prefix", "gqa")
-# Query heads per KV head the kernel is built for (the reference's grouped kernel takes
-# powers of two up to 16, tree_gqa.py:124-126).
-SUPPORTED_GROUPS = (1, 2, 4, 8, 16)
+# Query heads per KV head the MFMA kernel is built for (the reference's grouped kernel takes
+# powers of two up to 16, tree_gqa.py:124-126; 3, 5, 6 and 7 are the GQA ratios of other
+# Qwen-family checkpoints, e.g. 40 query over 8 KV heads).  Other ratios run the FP32 kernel.
+SUPPORTED_GROUPS = (1, 2, 3, 4, 5, 6, 7, 8, 16)
 _FP32_ROUTE = "fp32"     # cache entries of batches that run the FP32 kernel
 _derived: dict[int, dict] = {}
 _derived_lock = threading.Lock()

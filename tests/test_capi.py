@@ -70,7 +70,7 @@ def test_entry_points_reject_bad_arguments_without_a_device():
         make_plan([10], [4], 8, 48, 256, queries_per_kv=4)
     with pytest.raises(ValueError, match="no tree nodes"):
         make_plan([10], [0], 8, 256, 256, queries_per_kv=4)
-    for bad_group in (0, 3, 6, 32):
+    for bad_group in (0, 9, 12, 32):
         with pytest.raises(ValueError, match="query heads per KV head"):
             make_plan([10], [4], 8, 256, 256, queries_per_kv=bad_group)
 
@@ -261,11 +261,11 @@ def test_plan_covers_every_row_and_key_once(prefixes, counts, kv_heads, chunk):
     check_plan_covers(prefixes, counts, kv_heads, 256, chunk)
 
 
-@pytest.mark.parametrize("groups", [1, 2, 8, 16])
+@pytest.mark.parametrize("groups", [1, 2, 3, 5, 6, 7, 8, 16])
 @pytest.mark.parametrize("kv_heads", [1, 2, 8])
 def test_plan_covers_every_row_and_key_once_per_group_size(groups, kv_heads):
-    """Items of (8 / hpw) * (32 / G) nodes: 256 nodes at G = 1 down to 16 at G = 16, and
-    the two-head form for trees up to half that."""
+    """Items of (8 / hpw) * floor(32 / G) nodes: 256 nodes at G = 1 down to 16 at G = 16
+    (48 at G = 5), and the two-head form for trees up to half that."""
     prefixes = [0, 1, 63, 64, 65, 255, 256, 257, 4096, 300, 9000]
     counts = [1, 2, 16, 17, 32, 33, 64, 65, 512, 129, 256]
     for chunk in (0, 64):
@@ -358,7 +358,8 @@ def test_signature_capacity_covers_every_node_count_vector():
         count = int(rng.integers(1, 9))
         high = int(rng.choice([40, 130, 300, 1024]))
         vectors.append(tuple(int(x) for x in rng.integers(1, high + 1, size=count)))
-    cases = [(8, 0, 4), (1, 0, 4), (2, 0, 4), (8, 2048, 4), (8, 0, 1), (2, 0, 16), (1, 0, 8), (8, 2048, 2)]
+    cases = [(8, 0, 4), (1, 0, 4), (2, 0, 4), (8, 2048, 4), (8, 0, 1), (2, 0, 16), (1, 0, 8), (8, 2048, 2),
+             (8, 0, 5), (2, 0, 7), (1, 2048, 3)]
     for counts in vectors:
         for kv_heads, chunk, groups in cases:
             where = (counts, kv_heads, chunk, groups)

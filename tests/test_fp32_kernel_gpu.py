@@ -9,7 +9,7 @@ oracle: FP32 output within the reference's FP32 qualification bound
 output within the north-star gate.  Pools carry NaN in every unused row.
 
 Cases: f32 Q/K/V through every FP32 entry; head sizes 64, 96, 256 and 512; query groups
-3, 6 and 32; page sizes 16 and 48; a 1500-node causal chunk; a K/V pool whose head
+9, 12 and 32; page sizes 16 and 48; a 1500-node causal chunk; a K/V pool whose head
 dimension is strided; finite qq_bias values (legacy entry; the packed MFMA path flags
 them); bad pages; and a captured launch that follows staged metadata.
 """
@@ -116,7 +116,7 @@ def test_head_sizes(head_dim):
               scale=scale)
 
 
-@pytest.mark.parametrize("groups,kv_heads", [(3, 2), (6, 1), (32, 1)])
+@pytest.mark.parametrize("groups,kv_heads", [(9, 2), (12, 1), (32, 1)])
 def test_query_groups_beyond_the_mfma_kernel(groups, kv_heads):
     q, k, v, meta, *_ = make_case((129, 7, 700), (9, 33, 20), kv_heads=kv_heads, groups=groups, seed=groups)
     assert not _mfma_geometry(q, k, v, meta)

@@ -1,11 +1,13 @@
-"""Every query-group size the kernel is built for, G in {1, 2, 4, 8, 16} (GPU).
+"""Every query-group size the MFMA kernel is built for, G in 1..8 and 16 (GPU).
 
 The reference's grouped kernel takes any power of two up to 16 query heads per KV head
-(tree_gqa.py:124-126) and its reference kernel any divisor; this build instantiates
-the MFMA kernel for each power of two.  A work item is 8 waves x 32 score rows, so it
-holds (8 / HPW) * (32 / G) tree nodes of each of its HPW KV heads: 256 nodes at G = 1
-down to 16 at G = 16, with two KV heads per item for trees of at most half that.  The
-node counts below sit on both sides of those limits for every G.
+(tree_gqa.py:124-126) and its FP32 kernel any divisor; this build instantiates the MFMA
+kernel for G = 1..8 and 16 (the powers of two and the GQA ratios of other Qwen-family
+checkpoints) and runs other ratios on the FP32 kernel.  A work item is 8 waves x 32 score
+rows, so it holds (8 / HPW) * floor(32 / G) tree nodes of each of its HPW KV heads: 256
+nodes at G = 1 down to 16 at G = 16, with two KV heads per item for trees of at most
+half that; when G does not divide 32, each wave's last 32 - floor(32 / G) * G rows are
+padding.  The node counts below sit on both sides of those limits for every G.
 
 Per G:
   * bf16 output within the north-star gate of the fp64 oracle on every row (auto
@@ -38,7 +40,7 @@ from test_legacy_exact_gpu import legacy_call
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 SCALE = 128 ** -0.5
-GROUPS = (1, 2, 8, 16)   # G = 4 is covered by every other GPU test
+GROUPS = (1, 2, 3, 5, 6, 7, 8, 16)   # G = 4 is covered by every other GPU test
 
 
 def nodes_per_item(hpw, groups):
@@ -133,7 +135,7 @@ def test_graphed_attention_equals_eager(groups):
     assert read_and_clear_status(DEV) == 0
 
 
-@pytest.mark.parametrize("groups", [1, 16])
+@pytest.mark.parametrize("groups", [1, 5, 16])
 def test_legacy_entry_equals_packed_fp32_entry(groups):
     q, k, v, meta, slots, masks, _ = fixture(groups)
     for r in range(meta.num_requests):
@@ -149,11 +151,11 @@ def test_legacy_entry_equals_packed_fp32_entry(groups):
 
 
 def test_other_group_sizes_take_the_fp32_kernel():
-    """Group sizes outside {1, 2, 4, 8, 16} run the FP32 kernel (tests/test_fp32_kernel_gpu.py
+    """Group sizes outside 1-8 and 16 run the FP32 kernel (tests/test_fp32_kernel_gpu.py
     checks its values); the grouped entry refuses them as the reference's does."""
     q, k, v, meta, *_ = reference_fixture(kv_heads=1, groups=4)
     assert _mfma_geometry(q, k, v, meta)
-    for heads in (3, 6, 32):
+    for heads in (9, 12, 32):
         other = torch.randn((q.shape[0], heads, 128), device=DEV).to(q.dtype)
         assert not _mfma_geometry(other, k, v, meta)
         out = packed_tree_attention(other, k, v, meta, SCALE, heads)

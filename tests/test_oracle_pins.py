@@ -145,7 +145,7 @@ def test_paged_oracle_equals_parent_chain_brute_force(seed, prefixes, counts):
     np.testing.assert_allclose(out, parent_chain_reference(case), rtol=1e-10, atol=1e-12)
 
 
-@pytest.mark.parametrize("groups,kv_heads", [(1, 3), (2, 2), (8, 2), (16, 1)])
+@pytest.mark.parametrize("groups,kv_heads", [(1, 3), (2, 2), (5, 2), (8, 2), (16, 1)])
 def test_paged_oracle_equals_brute_force_at_every_group_size(groups, kv_heads):
     """Query head h reads KV head h // G (block grouping) for every G the kernel takes."""
     case = random_case(11 + groups, [70, 0, 33], [9, 5, 12], kv_heads=kv_heads, groups=groups)
