@@ -95,3 +95,35 @@ def test_legacy_entry_rejections_before_any_device_work():
         paged_tree_attention(q, k, v, None, None, torch.zeros(2), None, 1.0, 4, 256)
     with pytest.raises(ValueError, match="external jetspec kernel"):
         paged_tree_attention(q, k, v, None, None, torch.zeros(1), None, 1.0, 4, 256)
+
+
+def test_kernel_choice_follows_the_mfma_geometry():
+    """The drop-in's per-batch kernel choice (host logic): the MFMA kernel for bf16/f16,
+    head_dim 128, 1-8 or 16 query heads per KV head, page sizes that are multiples of 32,
+    trees of at most 1024 nodes and 16-byte aligned K/V rows; the FP32 kernel otherwise."""
+    from types import SimpleNamespace
+
+    from jetspec_amd.paged_backend import _mfma_geometry
+
+    def case(*, dtype=torch.bfloat16, groups=4, head_dim=128, block=256, nodes=(64,), kv=8, pool=None):
+        q = torch.zeros(2, groups * kv, head_dim, dtype=dtype)
+        k = torch.zeros(4, block, kv, head_dim, dtype=dtype) if pool is None else pool
+        meta = SimpleNamespace(block_size=block, node_counts_host=tuple(nodes))
+        return _mfma_geometry(q, k, k, meta)
+
+    assert case()
+    assert case(dtype=torch.float16)
+    for groups in (1, 2, 3, 5, 6, 7, 8, 16):
+        assert case(groups=groups), groups
+    assert case(nodes=(1024, 3)) and case(block=32) and case(block=512)
+    assert not case(dtype=torch.float32)
+    for groups in (9, 12, 32):
+        assert not case(groups=groups), groups
+    for head_dim in (64, 96, 256):
+        assert not case(head_dim=head_dim), head_dim
+    assert not case(block=16) and not case(block=48)
+    assert not case(nodes=(64, 1025))
+    wide = torch.zeros(4, 256, 8, 256, dtype=torch.bfloat16)
+    assert not case(pool=wide[..., ::2])                     # strided head dimension
+    assert not case(pool=wide[..., 1:129])                   # rows not 16-byte aligned
+    assert case(pool=wide[..., 128:])                        # aligned view of a wider row
