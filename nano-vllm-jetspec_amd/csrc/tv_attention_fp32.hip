@@ -2,21 +2,23 @@
 //
 // The MI355X form of the reference's scalar FP32 kernel (paged_backend.py:116-213) and
 // of its legacy slot-addressed form (paged_backend.py:20-113): the path for batches the
-// MFMA kernel does not take (f32 operands, head sizes other than 128, query groups
-// other than 1/2/4/8/16, page sizes that are not multiples of 32, trees above 1024
-// nodes, finite qq_bias values).  The reference runs one program per (packed row,
-// query head); here one wave owns a (packed row, KV head) and its G query heads, so
-// every K/V row it loads serves all G heads.
+// MFMA kernel does not take (f32 operands, head sizes other than 128, query groups the
+// MFMA kernel is not built for, page sizes that are not multiples of 32, trees above
+// 1024 nodes, finite qq_bias values).  The reference runs one program per (packed row,
+// query head).  Here a workgroup of four waves owns four consecutive rows of one request
+// and one KV head with its G query heads, so every K/V row it loads serves 4 x G rows.
 //
-// Per 64-key tile of the visible range [0, P + local]:
-//   lane k resolves key k's slot (page table, prefix slot vector or tree slot) and its
-//   bias, and computes the G scores q_g . K[key] from its own K row against the wave's
-//   Q rows in LDS (broadcast reads);
-//   each head's online softmax runs as wave reductions (max, then sum), in fp32;
-//   for P.V the lanes own head dimensions (lane + 64 j) and walk the tile's keys:
-//   coalesced V row loads, probabilities read from LDS.
-// Accumulators: G_pass x DJ floats per lane with DJ = ceil(D / 64); query heads beyond
-// G_pass = min(16, 64 / DJ) take further passes over the keys.
+// Per tile of TK keys (64 up to head_dim 128) of the group's visible range:
+//   the first TK threads resolve the keys' slots (page table, prefix slot vector or tree
+//   slot); all threads stage the K and V rows into LDS as float (coalesced loads, rows
+//   padded to an odd pitch);
+//   each wave, for its own row: lane k scores key k against the row's G query vectors
+//   (LDS broadcast reads), adds the tree key's bias, runs each head's online softmax as
+//   wave reductions (max, then sum) in fp32, and for P.V the lanes own head dimensions
+//   (lane + 64 j) and walk the tile's keys.
+// Accumulators: G_pass x DJ floats per lane with DJ = ceil(D / 64) and G_pass the smallest
+// power of two >= G up to min(16, 64 / DJ); query heads beyond G_pass take further passes
+// over the keys.
 #include <math.h>
 #include <stdint.h>
 
@@ -85,38 +87,167 @@ __device__ __forceinline__ void store_value(const Fp32Params& p, int64_t index, 
     }
 }
 
-// T: operand type; DJ: head dimensions per lane (D <= 64 * DJ).
-template <typename T, int DJ>
-__global__ void __launch_bounds__(kWave)
-tree_attention_fp32_kernel(const Fp32Params p) {
-    constexpr int GP = (kWave / DJ < 16) ? kWave / DJ : 16;   // query heads per pass
-    constexpr int PITCH = kWave * DJ;                          // LDS row of one query head
-    __shared__ __attribute__((aligned(16))) float q_lds[GP * PITCH];
-    __shared__ float p_lds[GP * kWave];
-    __shared__ int64_t slot_lds[kWave];
+constexpr int kRowsPerGroup = 4;    // waves per workgroup: consecutive rows of one request
+constexpr int kThreadsFp32 = kWave * kRowsPerGroup;
 
-    const int lane = threadIdx.x;
-    const int64_t row = blockIdx.x;
+// The launch numbers the row groups of request r from start(r) = cu[r] / 4 + r on: the
+// ranges are disjoint and increasing (start(r + 1) - start(r) >= ceil(T_r / 4)), so a grid
+// of Q / 4 + R + 1 workgroups covers every group with at most one idle workgroup per
+// request, and consecutive workgroups (spread over the XCDs) all have work.
+__device__ __forceinline__ int64_t group_start(const int32_t* cu, int r) {
+    return static_cast<int64_t>(cu[r] / kRowsPerGroup) + r;
+}
+
+// The request whose group range holds workgroup b: the last r with start(r) <= b, by a
+// 64-way search of the wave (two rounds of loads up to 4096 requests).
+__device__ int request_of_group(const int32_t* cu, int num_requests, int64_t b) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int lo = 0, hi = num_requests;   // start(lo) <= b; the answer is in [lo, hi)
+    while (hi - lo > 1) {
+        const int step = (hi - lo + kWave - 1) / kWave;
+        const int r = lo + lane * step;
+        const bool le = r < hi && group_start(cu, r) <= b;
+        const uint64_t mask = __ballot(le);   // lanes 0 .. k set: start() increases with r
+        const int last = 63 - __builtin_clzll(mask | 1ull);
+        lo += last * step;
+        hi = min(hi, lo + step);
+    }
+    return lo;
+}
+
+// Keys per LDS tile: 64 up to head_dim 128, fewer above (the K and V tiles stay near 66 KiB).
+template <int DJ>
+struct TileShape {
+    static constexpr int TK = DJ <= 2 ? 64 : 64 * 2 / DJ;
+    static constexpr int PITCH = kWave * DJ;          // LDS row of one query head (floats)
+    // K/V rows padded by 4 floats: 16-byte aligned, and a lane-per-key 16-byte read of 16
+    // lanes covers the 64 banks once.
+    static constexpr int KV_PITCH = kWave * DJ + 4;
+    static constexpr int KPW = TK / kRowsPerGroup;    // keys each wave stages per tile
+};
+
+// A score more than this far above a row's reference maximum (natural-log units) raises
+// the maximum; below it probabilities stay <= e^8, which fp32 holds with its full
+// relative precision, so the result is the same online softmax with rare rescales.
+constexpr float kRaiseMargin = 8.f;
+
+// T: operand type; DJ: head dimensions per lane (D <= 64 * DJ); GP: query heads per pass
+// (the launch picks the smallest power of two >= G, at most 16 and at most 64 / DJ, so
+// G_pass x DJ accumulators fit).  Workgroup: rows local0 .. local0 + 3 of one request and
+// one KV head.  Software pipeline over tiles of TK keys: while tile t is computed, the K/V
+// loads of tile t + 1 (slots resolved one iteration earlier) and the slot lookups of
+// tile t + 2 are in flight; tile t's K/V rows, staged in LDS as float, serve all four
+// rows.  Each wave runs its own row: lane k scores key k against the row's G query
+// vectors, the row's reference maximum is raised only when a score exceeds it by
+// kRaiseMargin (a ballot; the wave reduction runs then), probabilities and per-lane sums
+// use it, and for P.V the lanes own head dimensions.
+template <typename T, int DJ, int GP>
+__global__ void __launch_bounds__(kThreadsFp32)
+tree_attention_fp32_kernel(const Fp32Params p) {
+    typedef TileShape<DJ> S;
+    constexpr int TK = S::TK, PITCH = S::PITCH, KV_PITCH = S::KV_PITCH, KPW = S::KPW;
+    static_assert(GP * DJ <= 64, "accumulators per lane");
+    static_assert(TK <= kThreadsFp32 && TK % 4 == 0, "one slot lookup per thread, 4-key P.V steps");
+    __shared__ __attribute__((aligned(16))) float q_lds[kRowsPerGroup][GP * PITCH];
+    __shared__ __attribute__((aligned(16))) float p_lds[kRowsPerGroup][GP * TK];
+    __shared__ __attribute__((aligned(16))) float k_lds[TK * KV_PITCH];
+    __shared__ __attribute__((aligned(16))) float v_lds[TK * KV_PITCH];
+    __shared__ int64_t kbase_lds[2][TK], vbase_lds[2][TK];   // element offsets of the rows, -1: missing
+
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int kvh = blockIdx.y;
-    const int r = p.q2r[row];
-    if (r < 0 || r >= p.num_requests) {
-        if (lane == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+    const int r = __builtin_amdgcn_readfirstlane(request_of_group(p.cu, p.num_requests, blockIdx.x));
+    const int local0 = static_cast<int>(blockIdx.x - group_start(p.cu, r)) * kRowsPerGroup;
+    const int P = p.plen[r], nodes = p.cnt[r];
+    if (local0 >= nodes) return;   // the gap after request r's groups
+    if (P < 0) {
+        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
     }
-    const int local = p.local[row];
-    const int P = p.plen[r], nodes = p.cnt[r];
-    if (local < 0 || local >= nodes || P < 0) {
-        if (lane == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+    const int64_t leader = static_cast<int64_t>(p.cu[r]) + local0;
+    const int rows = min(kRowsPerGroup, nodes - local0);
+    if (leader < 0 || leader + rows > p.total_queries) {
+        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
+    }
+    // This wave's row; the metadata must place a request's rows consecutively.
+    const int64_t row = leader + wave;
+    const int local = local0 + wave;
+    bool row_ok = wave < rows;
+    if (row_ok && (p.q2r[row] != r || p.local[row] != local)) {
+        if (lane == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+        row_ok = false;
     }
     const int D = p.head_dim, B = p.block_size, G = p.groups;
     const int64_t tree0 = p.cu[r];
     const int64_t bias_row = p.bias_off[r] + static_cast<int64_t>(local) * nodes;
-    const int seq = P + local + 1;   // positions past P + local are never visible
+    const int seq = P + local0 + rows;    // keys any row of the group can see
+    const int ntiles = (seq + TK - 1) / TK;
+    const int my_end = P + local + 1;     // this row's visible range
     const int64_t pool_slots = p.num_blocks * B;
     const T* q = static_cast<const T*>(p.q);
     const T* k = static_cast<const T*>(p.k);
     const T* v = static_cast<const T*>(p.v);
+
+    // Slot of key t0 + tid (threads < TK): the load, then the row offsets.
+    auto slot_load = [&](int t0) -> int64_t {
+        const int pos = t0 + tid;
+        if (tid >= TK || pos >= seq) return -1;
+        if (pos >= P) return p.tree_slots[tree0 + (pos - P)];
+        if (p.pslots) {
+            const int64_t at = static_cast<int64_t>(r) * p.ps_s0 + pos;
+            return p.ps_i64 ? static_cast<const int64_t*>(p.pslots)[at]
+                            : static_cast<int64_t>(static_cast<const int32_t*>(p.pslots)[at]);
+        }
+        const int64_t page = p.tables[static_cast<int64_t>(r) * p.t_s0 + pos / B];
+        return (page >= 0 && page < p.num_blocks) ? page * B + pos % B : -2;
+    };
+    auto slot_store = [&](int t0, int64_t slot, int buf) {
+        const int pos = t0 + tid;
+        if (tid >= TK) return;
+        int64_t kb = -1, vb = -1;
+        if (pos < seq) {
+            if (slot < 0 || slot >= pool_slots) {
+                set_status(p.status, TV_STATUS_BAD_PAGE);
+            } else {
+                const int64_t blk = slot / B, off = slot - blk * B;
+                kb = blk * p.k_s0 + off * p.k_s1 + static_cast<int64_t>(kvh) * p.k_s2;
+                vb = blk * p.v_s0 + off * p.v_s1 + static_cast<int64_t>(kvh) * p.v_s2;
+            }
+        }
+        kbase_lds[buf][tid] = kb;
+        vbase_lds[buf][tid] = vb;
+    };
+    // This thread's share of a tile's K and V: wave w stages keys w, w + 4, ..., its lanes
+    // along the head dimension (coalesced); every load is issued before any is used.
+    float kx[KPW][DJ], vx[KPW][DJ];
+    auto kv_load = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < KPW; ++i) {
+            const int key = wave + kRowsPerGroup * i;
+            const int64_t kb = kbase_lds[buf][key], vb = vbase_lds[buf][key];
+#pragma unroll
+            for (int j = 0; j < DJ; ++j) {
+                const int d = lane + kWave * j;
+                const bool ok = kb >= 0 && d < D;
+                kx[i][j] = ok ? to_float(k[kb + d * p.k_s3]) : 0.f;
+                vx[i][j] = ok ? to_float(v[vb + d * p.v_s3]) : 0.f;
+            }
+        }
+    };
+    auto kv_store = [&]() {
+#pragma unroll
+        for (int i = 0; i < KPW; ++i) {
+            const int key = wave + kRowsPerGroup * i;
+#pragma unroll
+            for (int j = 0; j < DJ; ++j) {
+                const int d = lane + kWave * j;
+                k_lds[key * KV_PITCH + d] = kx[i][j];
+                v_lds[key * KV_PITCH + d] = vx[i][j];
+            }
+        }
+    };
 
     for (int g0 = 0; g0 < G; g0 += GP) {
         const int gn = min(GP, G - g0);
@@ -124,10 +255,9 @@ tree_attention_fp32_kernel(const Fp32Params p) {
         for (int i = lane; i < GP * PITCH; i += kWave) {
             const int g = i / PITCH, d = i - g * PITCH;
             float x = 0.f;
-            if (g < gn && d < D) x = to_float(q[row * p.q_s0 + static_cast<int64_t>(head0 + g) * p.q_s1 + d]);
-            q_lds[i] = x;
+            if (row_ok && g < gn && d < D) x = to_float(q[row * p.q_s0 + static_cast<int64_t>(head0 + g) * p.q_s1 + d]);
+            q_lds[wave][i] = x;
         }
-        __syncthreads();
         float m[GP], l[GP], acc[GP][DJ];
 #pragma unroll
         for (int g = 0; g < GP; ++g) {
@@ -136,114 +266,132 @@ tree_attention_fp32_kernel(const Fp32Params p) {
 #pragma unroll
             for (int j = 0; j < DJ; ++j) acc[g][j] = 0.f;
         }
-        for (int t0 = 0; t0 < seq; t0 += kWave) {
-            // This lane's key: slot, bias and visibility.
-            const int pos = t0 + lane;
-            int64_t slot = -1;
-            float bias = 0.f;
-            bool visible = pos < seq;
-            if (visible) {
-                if (pos < P) {
-                    if (p.pslots) {
-                        const int64_t at = static_cast<int64_t>(r) * p.ps_s0 + pos;
-                        slot = p.ps_i64 ? static_cast<const int64_t*>(p.pslots)[at]
-                                        : static_cast<int64_t>(static_cast<const int32_t*>(p.pslots)[at]);
-                    } else {
-                        const int64_t page = p.tables[static_cast<int64_t>(r) * p.t_s0 + pos / B];
-                        slot = (page >= 0 && page < p.num_blocks) ? page * B + pos % B : -1;
-                    }
-                } else {
-                    slot = p.tree_slots[tree0 + (pos - P)];
+        // Pipeline prologue: slots of tiles 0 and 1, K/V loads of tile 0.
+        __syncthreads();   // the previous pass's LDS reads are done
+        slot_store(0, slot_load(0), 0);
+        __syncthreads();
+        kv_load(0);
+        if (ntiles > 1) slot_store(TK, slot_load(TK), 1);
+        for (int t = 0; t < ntiles; ++t) {
+            const int t0 = t * TK;
+            __syncthreads();   // tile t - 1's LDS reads are done; tile t + 1's slots are in LDS
+            kv_store();
+            __syncthreads();   // tile t is staged
+            if (t + 1 < ntiles) kv_load((t + 1) & 1);
+            const int64_t next_slot = t + 2 < ntiles ? slot_load(t0 + 2 * TK) : -1;
+            if (row_ok) {
+                const int pos = t0 + lane;
+                bool visible = lane < TK && pos < my_end && kbase_lds[t & 1][lane < TK ? lane : 0] >= 0;
+                float bias = 0.f;
+                if (visible && pos >= P) {
                     bias = p.bias[bias_row + (pos - P)];
+                    if (bias == -INFINITY) visible = false;
                 }
-                if (slot < 0 || slot >= pool_slots) {
-                    set_status(p.status, TV_STATUS_BAD_PAGE);
-                    visible = false;
-                } else if (bias == -INFINITY) {
-                    visible = false;
-                }
-            }
-            slot_lds[lane] = visible ? slot : -1;
-            float s[GP];
+                float sc[GP];
 #pragma unroll
-            for (int g = 0; g < GP; ++g) s[g] = 0.f;
-            if (visible) {
-                const T* kr = k + (slot / B) * p.k_s0 + (slot % B) * p.k_s1 + static_cast<int64_t>(kvh) * p.k_s2;
-                for (int d = 0; d < D; d += 4) {
-                    float kx[4];
+                for (int g = 0; g < GP; ++g) sc[g] = 0.f;
+                if (visible) {
+                    const float* kr = k_lds + (lane < TK ? lane : 0) * KV_PITCH;
+#pragma unroll 2
+                    for (int d = 0; d < D; d += 4) {
+                        const float4 kv4 = *reinterpret_cast<const float4*>(kr + d);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) kx[i] = d + i < D ? to_float(kr[(d + i) * p.k_s3]) : 0.f;
-#pragma unroll
-                    for (int g = 0; g < GP; ++g) {
-                        const float4 qv = *reinterpret_cast<const float4*>(&q_lds[g * PITCH + d]);
-                        s[g] = fmaf(qv.x, kx[0], s[g]);
-                        s[g] = fmaf(qv.y, kx[1], s[g]);
-                        s[g] = fmaf(qv.z, kx[2], s[g]);
-                        s[g] = fmaf(qv.w, kx[3], s[g]);
+                        for (int g = 0; g < GP; ++g) {
+                            const float4 qv = *reinterpret_cast<const float4*>(&q_lds[wave][g * PITCH + d]);
+                            sc[g] = fmaf(qv.x, kv4.x, sc[g]);
+                            sc[g] = fmaf(qv.y, kv4.y, sc[g]);
+                            sc[g] = fmaf(qv.z, kv4.z, sc[g]);
+                            sc[g] = fmaf(qv.w, kv4.w, sc[g]);
+                        }
                     }
-                }
-            }
-            // Online softmax per query head; a tile with no visible key leaves a head as it was.
-#pragma unroll
-            for (int g = 0; g < GP; ++g) {
-                const float score = visible ? fmaf(s[g], p.scale, bias) : -INFINITY;
-                const float m_new = fmaxf(m[g], wave_max(score));
-                const float m_ref = m_new == -INFINITY ? 0.f : m_new;
-                const float alpha = expf(m[g] - m_ref);
-                const float pr = expf(score - m_ref);
-                l[g] = l[g] * alpha + wave_sum(pr);
-#pragma unroll
-                for (int j = 0; j < DJ; ++j) acc[g][j] *= alpha;
-                m[g] = m_new;
-                p_lds[g * kWave + lane] = pr;
-            }
-            __syncthreads();
-            const int keys = min(kWave, seq - t0);
-            for (int kk = 0; kk < keys; ++kk) {
-                const int64_t sl = slot_lds[kk];
-                if (sl < 0) continue;
-                const T* vr = v + (sl / B) * p.v_s0 + (sl % B) * p.v_s1 + static_cast<int64_t>(kvh) * p.v_s2;
-                float vx[DJ];
-#pragma unroll
-                for (int j = 0; j < DJ; ++j) {
-                    const int d = lane + kWave * j;
-                    vx[j] = d < D ? to_float(vr[d * p.v_s3]) : 0.f;
                 }
 #pragma unroll
                 for (int g = 0; g < GP; ++g) {
-                    const float pg = p_lds[g * kWave + kk];
+                    const float score = visible ? fmaf(sc[g], p.scale, bias) : -INFINITY;
+                    if (__ballot(score > m[g] + kRaiseMargin)) {   // rare after the first tile
+                        const float m_new = fmaxf(m[g], wave_max(score));
+                        const float alpha = expf(m[g] - m_new);   // 0 while m[g] is -inf
+                        l[g] *= alpha;
 #pragma unroll
-                    for (int j = 0; j < DJ; ++j) acc[g][j] = fmaf(pg, vx[j], acc[g][j]);
+                        for (int j = 0; j < DJ; ++j) acc[g][j] *= alpha;
+                        m[g] = m_new;
+                    }
+                    const float pr = score == -INFINITY ? 0.f : expf(score - m[g]);
+                    l[g] += pr;
+                    if (lane < TK) p_lds[wave][g * TK + lane] = pr;
+                }
+                // P.V over the tile's keys (the wave reads only its own probabilities).
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int keys = min(TK, my_end - t0);
+                for (int kk = 0; kk < keys; kk += 4) {
+                    float vv[4][DJ];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+                        for (int j = 0; j < DJ; ++j) vv[u][j] = v_lds[(kk + u) * KV_PITCH + lane + kWave * j];
+                    }
+#pragma unroll
+                    for (int g = 0; g < GP; ++g) {
+                        const float4 pg = *reinterpret_cast<const float4*>(&p_lds[wave][g * TK + kk]);
+#pragma unroll
+                        for (int j = 0; j < DJ; ++j) {
+                            acc[g][j] = fmaf(pg.x, vv[0][j], acc[g][j]);
+                            acc[g][j] = fmaf(pg.y, vv[1][j], acc[g][j]);
+                            acc[g][j] = fmaf(pg.z, vv[2][j], acc[g][j]);
+                            acc[g][j] = fmaf(pg.w, vv[3][j], acc[g][j]);
+                        }
+                    }
                 }
             }
-            __syncthreads();   // slot_lds and p_lds are rewritten by the next tile
+            // Tile t's slot buffer was read by the loads issued in the previous iteration.
+            if (t + 2 < ntiles) slot_store(t0 + 2 * TK, next_slot, t & 1);
         }
+        if (row_ok) {
 #pragma unroll
-        for (int g = 0; g < GP; ++g) {
-            if (g >= gn) break;
-            const float inv = 1.f / l[g];
-            const int64_t base = row * p.o_s0 + static_cast<int64_t>(head0 + g) * p.o_s1;
+            for (int g = 0; g < GP; ++g) {
+                const float inv = 1.f / wave_sum(l[g]);
+                const int64_t base = row * p.o_s0 + static_cast<int64_t>(head0 + g) * p.o_s1;
 #pragma unroll
-            for (int j = 0; j < DJ; ++j) {
-                const int d = lane + kWave * j;
-                if (d < D) store_value(p, base + d, acc[g][j] * inv);
+                for (int j = 0; j < DJ; ++j) {
+                    const int d = lane + kWave * j;
+                    if (g < gn && d < D) store_value(p, base + d, acc[g][j] * inv);
+                }
             }
         }
-        __syncthreads();   // q_lds is rewritten by the next pass
+    }
+}
+
+template <typename T, int DJ>
+void launch_for_dims(const Fp32Params& p, const dim3& grid, hipStream_t s) {
+    constexpr int kMaxPass = 64 / DJ < 16 ? 64 / DJ : 16;
+    int gp = 2;
+    while (gp < p.groups && gp < kMaxPass) gp *= 2;
+    switch (gp) {
+        case 2: hipLaunchKernelGGL((tree_attention_fp32_kernel<T, DJ, 2>), grid, dim3(kThreadsFp32), 0, s, p); break;
+        case 4: hipLaunchKernelGGL((tree_attention_fp32_kernel<T, DJ, 4>), grid, dim3(kThreadsFp32), 0, s, p); break;
+        case 8: hipLaunchKernelGGL((tree_attention_fp32_kernel<T, DJ, 8>), grid, dim3(kThreadsFp32), 0, s, p); break;
+        default:
+            hipLaunchKernelGGL((tree_attention_fp32_kernel<T, DJ, kMaxPass>), grid, dim3(kThreadsFp32), 0, s, p);
+            break;
     }
 }
 
 template <typename T>
 void launch_for_type(const Fp32Params& p, int32_t kv_heads, hipStream_t s) {
-    const dim3 grid(static_cast<uint32_t>(p.total_queries), static_cast<uint32_t>(kv_heads));
+    // One workgroup per group of four rows of a request (group_start); the grid depends
+    // only on the packed row and request counts, which a captured graph keeps fixed.
+    const int64_t groups = static_cast<int64_t>(p.total_queries) / kRowsPerGroup + p.num_requests + 1;
+    const dim3 grid(static_cast<uint32_t>(groups), static_cast<uint32_t>(kv_heads));
     if (p.head_dim <= 64) {
-        hipLaunchKernelGGL((tree_attention_fp32_kernel<T, 1>), grid, dim3(kWave), 0, s, p);
+        launch_for_dims<T, 1>(p, grid, s);
     } else if (p.head_dim <= 128) {
-        hipLaunchKernelGGL((tree_attention_fp32_kernel<T, 2>), grid, dim3(kWave), 0, s, p);
+        launch_for_dims<T, 2>(p, grid, s);
     } else if (p.head_dim <= 256) {
-        hipLaunchKernelGGL((tree_attention_fp32_kernel<T, 4>), grid, dim3(kWave), 0, s, p);
+        launch_for_dims<T, 4>(p, grid, s);
     } else {
-        hipLaunchKernelGGL((tree_attention_fp32_kernel<T, 8>), grid, dim3(kWave), 0, s, p);
+        launch_for_dims<T, 8>(p, grid, s);
     }
 }
 
