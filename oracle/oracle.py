@@ -28,6 +28,10 @@ closed forms and an independent brute force; see the header of that file.
 rope_scatter_hf is pinned against torch's eager CPU bf16/fp32 arithmetic, which is the
 expected value of the reference's own test (tests/test_jetspec_tree_fusion.py:21-32),
 and against the reference's rounding witness (:117-126).
+
+Parity unpinned: accept_walk's equivalence with the un-vendored jetspec dependency's
+gpu_tree_accept (pyproject.toml:27-29) beyond the reference's duplicate-sibling KAT and
+the depth-cap closed form; that package is not installed and cannot be fetched here.
 """
 from __future__ import annotations
 
