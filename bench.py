@@ -60,6 +60,10 @@ def parse_args():
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
                              "launches); 'all' adds the rope_scatter, accept and graph legs")
+    parser.add_argument("--operands", choices=("normal", "constant", "zero"), default="normal",
+                        help="diagnostic: replace the N(0,1) Q/K/V values by constants or zeros (same shapes, "
+                             "pages, trees, instructions and bytes) to show the part's data-dependent clock; "
+                             "the headline is 'normal'")
     return parser.parse_args()
 
 
@@ -309,6 +313,14 @@ def run_verify(args, torch):
     batch = builder("cuda", **kwargs)
     meta = batch.metadata
     stream = torch.cuda.current_stream()
+    if args.operands != "normal":
+        # Every pool row and query gets the same value (zeros, or 0.5 / 0.25 / -0.5): the
+        # work is unchanged, only the operand bits stop toggling.
+        values = {"constant": (0.5, 0.25, -0.5), "zero": (0.0, 0.0, 0.0)}[args.operands]
+        for tensor, value in zip((batch.q, batch.k_pool, batch.v_pool), values):
+            tensor.fill_(value)
+        batch.new_k.fill_(values[1])
+        batch.new_v.fill_(values[2])
 
     def step(events=None):
         if events is not None:
@@ -348,7 +360,9 @@ def run_verify(args, torch):
         "metric": METRIC, "value": tokens * args.steps / elapsed, "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": elapsed * 1e3 / args.steps,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) bf16 Q/K/V, seeded parent arrays, permuted page pool)",
+        "data": ("synthetic (seeded N(0,1) bf16 Q/K/V, seeded parent arrays, permuted page pool)"
+                 if args.operands == "normal" else
+                 f"synthetic, diagnostic {args.operands} Q/K/V values (seeded parent arrays, permuted page pool)"),
         "config": {"workload": WORKLOADS[args.config], "requests": meta.num_requests,
                    "tree_rows_per_step": tokens, "prefix_tokens": sum(meta.prefix_lengths),
                    "q_heads": batch.q_heads, "kv_heads": batch.kv_heads, "head_dim": 128,
@@ -372,7 +386,7 @@ def run_verify(args, torch):
     probe = copy_probe(torch)
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]
-    if args.cpu_requests > 0 and args.config in (1, 2, 4, 5):
+    if args.cpu_requests > 0 and args.config in (1, 2, 4, 5) and args.operands == "normal":
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_requests)
     return result
 
