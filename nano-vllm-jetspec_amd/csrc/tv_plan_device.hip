@@ -61,22 +61,38 @@ __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) { return (x + 
 // planner uses the same weights.
 __device__ __forceinline__ int64_t cost_weight(int hpw) { return hpw == 2 ? 5 : 4; }
 
+constexpr int kPlanWaves = kPlanThreads / 64;
+
 // Block-wide exclusive scan of one int per thread (kPlanThreads threads); returns the
-// thread's prefix and writes the total to *total.
+// thread's prefix and writes the total to *total.  A scan within each wave (lane
+// shuffles), then the wave totals through LDS: two barriers.
 __device__ int64_t block_scan(int64_t v, int64_t* scratch, int64_t* total) {
-    const int t = threadIdx.x;
-    scratch[t] = v;
-    __syncthreads();
-    for (int off = 1; off < kPlanThreads; off <<= 1) {
-        const int64_t add = t >= off ? scratch[t - off] : 0;
-        __syncthreads();
-        scratch[t] += add;
-        __syncthreads();
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    int64_t x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t y = __shfl_up(x, off);
+        if (lane >= off) x += y;
     }
-    const int64_t inclusive = scratch[t];
-    if (t == kPlanThreads - 1) *total = inclusive;
+    if (lane == 63) scratch[w] = x;
     __syncthreads();
-    return inclusive - v;
+    int64_t before = 0, all = 0;
+#pragma unroll
+    for (int k = 0; k < kPlanWaves; ++k) {
+        const int64_t s = scratch[k];
+        before += k < w ? s : 0;
+        all += s;
+    }
+    if (t == 0) *total = all;
+    __syncthreads();   // *total is visible, and every thread has read `scratch`
+    return before + x - v;
+}
+
+// Sum over one wave (returned to every lane).
+__device__ __forceinline__ int64_t wave_sum(int64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
 }
 
 // Block-wide sum of one int64 per thread (kPlanThreads threads), returned to all.
@@ -109,6 +125,7 @@ plan_device_kernel(const PlanArgs a) {
     __shared__ int32_t req_item_off[kMaxPlanRequests], req_group_off[kMaxPlanRequests], req_slot_off[kMaxPlanRequests];
     __shared__ int32_t stream_id[kMaxSortItems];   // (request, head group, chunk) of each sorted item
     __shared__ int shared_flag;
+    __shared__ int32_t probe_fits[kPlanWaves];
     const int t = threadIdx.x;
     const int R = a.num_requests;
     const int B = a.block_size;
@@ -138,29 +155,46 @@ plan_device_kernel(const PlanArgs a) {
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * B) / 32 * 32;
 
     // 1b. The host's refit of the chunk target when the items leave the last of at most
-    // kFillRounds rounds part-empty: the same bisection, each probe a block sum.
-    auto items_for = [&](int64_t tau) -> int64_t {
-        int64_t n = 0;
-        for (int r = t; r < R; r += kPlanThreads) {
-            const int64_t p = max(0, a.prefix_lens[r]);
-            const int nodes = max(1, min(1024, a.node_counts[r]));
-            const int hpw = heads_per_group(nodes, a.num_kv_heads, a.qpk);
-            const int npw = nodes_per_item(hpw, a.qpk);
-            const int64_t units = static_cast<int64_t>((a.num_kv_heads + hpw - 1) / hpw) * ((nodes + npw - 1) / npw);
-            const int64_t chunk = chunk_for(p, hpw, tau, max_chunk);
-            n += units * (p > 0 ? (p + chunk - 1) / chunk : 1);
-        }
-        return block_sum(n, scan);
+    // kFillRounds rounds part-empty: the smallest target whose item count fits the same
+    // rounds.  The count falls as the target grows, so any search finds the host's
+    // bisection result; here each of the 16 waves probes one target per round (a
+    // 17-way search, one barrier per round).
+    auto request_items = [&](int r, int64_t tau) -> int64_t {
+        const int64_t p = max(0, a.prefix_lens[r]);
+        const int nodes = max(1, min(1024, a.node_counts[r]));
+        const int hpw = heads_per_group(nodes, a.num_kv_heads, a.qpk);
+        const int npw = nodes_per_item(hpw, a.qpk);
+        const int64_t units = static_cast<int64_t>((a.num_kv_heads + hpw - 1) / hpw) * ((nodes + npw - 1) / npw);
+        const int64_t chunk = chunk_for(p, hpw, tau, max_chunk);
+        return units * (p > 0 ? (p + chunk - 1) / chunk : 1);
     };
     int64_t tau = target;
     if (a.chunk_keys == 0) {
-        const int64_t now = items_for(target);
+        int64_t now = 0;
+        for (int r = t; r < R; r += kPlanThreads) now += request_items(r, target);
+        now = block_sum(now, scan);
         const int64_t rounds = (now + a.compute_units - 1) / a.compute_units;
         if (now > a.compute_units && rounds <= kFillRounds) {
-            int64_t lo = 1, hi = target;
+            const int64_t limit = rounds * a.compute_units;
+            const int lane = t & 63, w = t >> 6;
+            int64_t lo = 1, hi = target;   // items(hi) <= limit; the answer is in [lo, hi]
             while (lo < hi) {
-                const int64_t mid = lo + (hi - lo) / 2;
-                if (items_for(mid) <= rounds * a.compute_units) hi = mid; else lo = mid + 1;
+                const int64_t span = hi - lo;
+                const int64_t probe = lo + span * (w + 1) / (kPlanWaves + 1);   // in [lo, hi)
+                int64_t n = 0;
+                for (int r = lane; r < R; r += 64) n += request_items(r, probe);
+                n = wave_sum(n);
+                if (lane == 0) probe_fits[w] = n <= limit ? 1 : 0;
+                __syncthreads();
+                int64_t new_lo = lo, new_hi = hi;
+#pragma unroll
+                for (int k = 0; k < kPlanWaves; ++k) {
+                    const int64_t pk = lo + span * (k + 1) / (kPlanWaves + 1);
+                    if (probe_fits[k]) new_hi = min(new_hi, pk); else new_lo = max(new_lo, pk + 1);
+                }
+                __syncthreads();   // every thread has read probe_fits
+                lo = new_lo;
+                hi = new_hi;
             }
             tau = lo;
         }
@@ -259,7 +293,18 @@ plan_device_kernel(const PlanArgs a) {
                     }
                 }
             }
-            __syncthreads();
+            // A stride below 64 pairs elements that one wave owns (e and e ^ stride differ
+            // only in bits below 64, and thread t owns e = t + k * kPlanThreads).  Between
+            // two such stages the wave's own LDS ordering is enough; a workgroup barrier
+            // precedes and follows every stage whose pairs cross waves, and the last stage.
+            const int next_stride = stride > 1 ? stride >> 1 : size;
+            if (stride < 64 && next_stride < 64 && size < npow) {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            } else {
+                __syncthreads();
+            }
         }
     }
 
