@@ -227,14 +227,18 @@ commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* _
 // source is some row's destination or its destination some row's source; a clean
 // row's source is never written and its destination never read by any row, so it
 // can be copied directly whatever the other rows do.  Workgroups (x >= 1, y) copy
-// the clean rows among rows 8(x-1)..8(x-1)+7 of plane y; workgroup (0, 0) finds the
-// dirty rows and moves them through the workspace (gather all, barrier, scatter
-// all), the reference's order.  Every workgroup validates every slot first, so an
-// invalid map writes nothing anywhere.  Each copy workgroup tests its 8 rows against
-// every slot (8n compares, its share of the n slots loaded once), so the one-launch form
+// the clean rows among rows R(x-1)..R(x-1)+R-1 of plane y (R = kFusedRows); workgroup
+// (0, 0) finds the dirty rows and moves them through the workspace (gather all,
+// barrier, scatter all), the reference's order.  Every workgroup validates every slot
+// first, so an invalid map writes nothing anywhere.  Each copy workgroup tests its R rows
+// against every slot (R n compares, its share of the n slots loaded once), so the one-launch form
 // is kept to n <= 512, where that costs less than a second launch; larger batches take
 // commit_check + commit_move.
 constexpr int64_t kFusedMaxSlots = 512;
+// Slot rows of one plane per copier workgroup: 4 (more, smaller workgroups) measured 20.1 us
+// against 22.7 us at 8 and 24.3 us at 16 for config 3 with the caches evicted first, and the
+// same 15.8 us warm.
+constexpr int kFusedRows = 4;
 constexpr int kFusedHash = 2 * kFusedMaxSlots;   // open-addressing slots per hash set (load <= 1/2)
 
 // Open-addressing set of non-negative 32-bit slots in LDS (empty entries are -1),
@@ -325,13 +329,13 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
     // Clean-row copier for rows i0..i0+nrows-1 of plane blockIdx.y.  Its own rows'
     // slots and this thread's share of all slots are loaded together, so validity and
     // dirtiness cost one round trip before the copy.
-    __shared__ int64_t row_src[kMoveRows], row_dst[kMoveRows];
+    __shared__ int64_t row_src[kFusedRows], row_dst[kFusedRows];
     __shared__ uint32_t skip;
-    const int32_t i0 = (blockIdx.x - 1) * kMoveRows;
-    const int32_t nrows = n - i0 < kMoveRows ? n - i0 : kMoveRows;
-    int64_t my_s[kMoveRows], my_d[kMoveRows];
+    const int32_t i0 = (blockIdx.x - 1) * kFusedRows;
+    const int32_t nrows = n - i0 < kFusedRows ? n - i0 : kFusedRows;
+    int64_t my_s[kFusedRows], my_d[kFusedRows];
 #pragma unroll
-    for (int r = 0; r < kMoveRows; ++r) {
+    for (int r = 0; r < kFusedRows; ++r) {
         my_s[r] = r < nrows ? src[i0 + r] : -1;
         my_d[r] = r < nrows ? dst[i0 + r] : -1;
     }
@@ -342,7 +346,7 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
         const int64_t a = src[k], b = dst[k];
         bad |= (a < 0 || a >= pool_slots || b < 0 || b >= pool_slots);
 #pragma unroll
-        for (int r = 0; r < kMoveRows; ++r) {
+        for (int r = 0; r < kFusedRows; ++r) {
             if (r < nrows && (my_s[r] == b || my_d[r] == a)) mine |= 1u << r;
         }
     }
@@ -569,7 +573,7 @@ extern "C" int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6], c
     hipStream_t s = as_stream(stream);
     int rc;
     if (num_slots <= kFusedMaxSlots && 2 * layers <= 65535 && pool_slots < (int64_t{1} << 31)) {
-        const dim3 grid(static_cast<uint32_t>((num_slots + kMoveRows - 1) / kMoveRows + 1),
+        const dim3 grid(static_cast<uint32_t>((num_slots + kFusedRows - 1) / kFusedRows + 1),
                         static_cast<uint32_t>(2 * layers));
         switch (unit) {
             case 16: hipLaunchKernelGGL(commit_fused_kernel<u32x4>, grid, dim3(kMoveThreads), 0, s, g, source_slots,
