@@ -5,6 +5,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "tv_attention.h"
@@ -19,10 +20,8 @@ namespace {
 // maximum m_s with sum l_s: the result is sum_s w_s O_s / sum_s w_s l_s with
 // w_s = 2^((m_s - max m) * c).
 template <typename T>
-__global__ void __launch_bounds__(256)
-merge_partials_kernel(const AttnParams p) {
-    if (p.counts && static_cast<int>(blockIdx.x) >= p.counts[1]) return;
-    const int32_t* gr = p.groups + 8 * blockIdx.x;
+__device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
+    const int32_t* gr = p.groups + 8 * static_cast<int64_t>(group);
     const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
     if (r < 0 || r >= p.num_requests) return;
     const int wph = 8 / hpw;
@@ -78,6 +77,18 @@ merge_partials_kernel(const AttnParams p) {
     if (head >= p.num_kv_heads || node >= tn || c >= nw * G) return;   // c >= nw * G: padding row
     const float inv = 1.f / l;
     store_out4<T>(p, qbase + node, qh, 4 * quad, o * inv);
+}
+
+// Grid (groups, 32) for a host plan.  A device-built plan (graph capture) launches at most
+// kMergeGridCap workgroup columns and the columns loop over the live group count, so a
+// signature-wide group capacity costs no flood of empty workgroups.
+constexpr int kMergeGridCap = 128;
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+merge_partials_kernel(const AttnParams p) {
+    const int count = p.counts ? p.counts[1] : static_cast<int>(gridDim.x);
+    for (int group = blockIdx.x; group < count; group += gridDim.x) merge_group<T>(p, group);
 }
 
 __global__ void __launch_bounds__(256)
@@ -287,10 +298,11 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
         default: launch_tree_attention_g16(p, a->num_items, bf16, exact, s); break;
     }
     if (a->num_groups > 0) {
+        const int columns = a->device_counts ? std::min(a->num_groups, kMergeGridCap) : a->num_groups;
         if (bf16) {
-            hipLaunchKernelGGL(merge_partials_kernel<__bf16>, dim3(a->num_groups, kRowsPerItem / 8), dim3(256), 0, s, p);
+            hipLaunchKernelGGL(merge_partials_kernel<__bf16>, dim3(columns, kRowsPerItem / 8), dim3(256), 0, s, p);
         } else {
-            hipLaunchKernelGGL(merge_partials_kernel<_Float16>, dim3(a->num_groups, kRowsPerItem / 8), dim3(256), 0, s, p);
+            hipLaunchKernelGGL(merge_partials_kernel<_Float16>, dim3(columns, kRowsPerItem / 8), dim3(256), 0, s, p);
         }
     }
     return check_launch("tree_attention");
