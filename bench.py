@@ -60,10 +60,11 @@ def parse_args():
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
                              "launches); 'all' adds the rope_scatter, accept and graph legs")
-    parser.add_argument("--operands", choices=("normal", "constant", "zero"), default="normal",
+    parser.add_argument("--operands", choices=("normal", "constant", "zero", "zero-q", "zero-kv"), default="normal",
                         help="diagnostic: replace the N(0,1) Q/K/V values by constants or zeros (same shapes, "
                              "pages, trees, instructions and bytes) to show the part's data-dependent clock; "
-                             "the headline is 'normal'")
+                             "'zero-q' zeroes only Q (random K/V still cross HBM and LDS), 'zero-kv' only the "
+                             "K/V pool and new rows (random Q); the headline is 'normal'")
     return parser.parse_args()
 
 
@@ -314,13 +315,16 @@ def run_verify(args, torch):
     meta = batch.metadata
     stream = torch.cuda.current_stream()
     if args.operands != "normal":
-        # Every pool row and query gets the same value (zeros, or 0.5 / 0.25 / -0.5): the
-        # work is unchanged, only the operand bits stop toggling.
-        values = {"constant": (0.5, 0.25, -0.5), "zero": (0.0, 0.0, 0.0)}[args.operands]
+        # The chosen tensors get one value in every element (zeros, or 0.5 / 0.25 / -0.5):
+        # the work is unchanged, only those operand bits stop toggling.
+        values = {"constant": (0.5, 0.25, -0.5), "zero": (0.0, 0.0, 0.0), "zero-q": (0.0, None, None),
+                  "zero-kv": (None, 0.0, 0.0)}[args.operands]
         for tensor, value in zip((batch.q, batch.k_pool, batch.v_pool), values):
-            tensor.fill_(value)
-        batch.new_k.fill_(values[1])
-        batch.new_v.fill_(values[2])
+            if value is not None:
+                tensor.fill_(value)
+        if values[1] is not None:
+            batch.new_k.fill_(values[1])
+            batch.new_v.fill_(values[2])
 
     def step(events=None):
         if events is not None:
