@@ -214,6 +214,30 @@ def test_rejections_match_reference_contract():
         packed_tree_attention(q.cpu(), k, v, meta, 0.1, 4)
 
 
+@pytest.mark.parametrize("block", [32, 96])
+def test_prefix_chunks_at_the_page_cache_limit(block, monkeypatch):
+    """Work items whose prefix range spans the 511-512 page numbers a workgroup caches in
+    LDS: the plan is made as for a one-compute-unit device, so every long prefix is cut
+    at that cap (chunks starting mid-page included), against the fp64 oracle."""
+    from jetspec_amd import _device
+    from jetspec_amd.paged_backend import make_plan
+
+    prefixes, counts = (40000, 511 * block, 511 * block + 1, 5), (16, 64, 1, 33)
+    plan = make_plan(list(prefixes), list(counts), 2, block, 1, 0, queries_per_kv=4)
+    spans = [((kend - 1) // block - kbeg // block + 1) if kend > kbeg else 0
+             for _, _, _, kbeg, kend, _, _, _ in plan["items"].tolist()]
+    assert 511 <= max(spans) <= 512
+    monkeypatch.setattr(_device, "compute_units", lambda index: 1)
+    q, k, v, meta, *_ = reference_fixture(prefixes, counts, kv_heads=2, block=block, seed=77)
+    print(f"[page cap] block={block} items={plan['num_items']} max pages={max(spans)}", flush=True)
+    out = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item(), "NaN padding was read"
+    expect = oracle_rows(q, k, v, meta, 128 ** -0.5, list(range(meta.num_requests)), rows_per_request=6)
+    assert_within_gate(out, expect, f"page cap, block {block}")
+    assert read_and_clear_status(q.device) == 0
+
+
 @pytest.mark.parametrize("config", ["config4", "config5"])
 def test_large_configs_sampled_rows(config):
     batch = getattr(workloads, config)(DEV)

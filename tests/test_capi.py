@@ -272,6 +272,25 @@ def test_plan_covers_every_row_and_key_once_per_group_size(groups, kv_heads):
         check_plan_covers(prefixes, counts, kv_heads, 256, chunk, groups=groups)
 
 
+MAX_CHUNK_PAGES = 512   # page numbers one work item caches in LDS
+
+
+@pytest.mark.parametrize("block", [32, 96, 256])
+def test_plan_chunks_fit_the_page_cache(block):
+    """However long a prefix and however much work per compute unit, no item's prefix range
+    spans more than the 512 page numbers a workgroup caches, wherever the range starts; with
+    few compute units the cap is what bounds the chunks."""
+    prefixes = [200000, 70000, 511 * block, 511 * block + 1, 5, 0]
+    counts = [16, 64, 1, 32, 8, 3]
+    for cus in (1, 8, 256):
+        plan = check_plan_covers(prefixes, counts, 2, cus, block=block)
+        spans = [((kend - 1) // block - kbeg // block + 1) if kend > kbeg else 0
+                 for _, _, _, kbeg, kend, _, _, _ in plan["items"].tolist()]
+        assert max(spans) <= MAX_CHUNK_PAGES
+        if cus == 1:
+            assert max(spans) >= MAX_CHUNK_PAGES - 1, "the page cap binds when each unit has long work"
+
+
 def test_plan_at_benchmark_shapes():
     rng = np.random.default_rng(4)
     prefixes = [int(x) for x in rng.integers(8192, 32769, size=64)]
