@@ -65,6 +65,10 @@ def parse_args():
                              "pages, trees, instructions and bytes) to show the part's data-dependent clock; "
                              "'zero-q' zeroes only Q (random K/V still cross HBM and LDS), 'zero-kv' only the "
                              "K/V pool and new rows (random Q); the headline is 'normal'")
+    parser.add_argument("--sustain", type=float, default=0.0,
+                        help="diagnostic: after the timed steps, run the attention back to back for this many "
+                             "seconds (so power and clock telemetry can be read while it runs) and report the "
+                             "sustained time per launch")
     return parser.parse_args()
 
 
@@ -304,6 +308,23 @@ def graph_leg(batch, torch, steps: int, warmup: int, layers: int = 36) -> dict:
             "speedup": eager_ms / replay_ms, "bitwise_equal": same}
 
 
+def sustain_leg(batch, torch, seconds: float) -> dict:
+    """The verify attention back to back for `seconds` of wall time, synchronising every 50
+    launches (a steady load for reading the part's power and clock telemetry)."""
+    from jetspec_amd import packed_tree_attention
+
+    meta = batch.metadata
+    print(f"[sustain] attention back to back for {seconds:.1f} s", file=sys.stderr, flush=True)
+    launches, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(50):
+            packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, batch.groups)
+        torch.cuda.synchronize()
+        launches += 50
+    wall = time.perf_counter() - t0
+    return {"seconds": wall, "launches": launches, "ms_per_launch": wall * 1e3 / launches}
+
+
 def run_verify(args, torch):
     from jetspec_amd import packed_tree_attention, read_and_clear_status, store_kvcache, workloads
 
@@ -387,6 +408,8 @@ def run_verify(args, torch):
         result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
         result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
+    if args.sustain > 0:
+        result["sustained"] = sustain_leg(batch, torch, args.sustain)
     probe = copy_probe(torch)
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]
