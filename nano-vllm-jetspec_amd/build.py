@@ -124,7 +124,31 @@ def build(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
         print("\n".join(messages), flush=True)
     check_m0_discipline(verbose, jobs)
     os.replace(tmp_so, OUTPUT)
+    build_examples(verbose)
     return OUTPUT
+
+
+EXAMPLES = HERE / "examples"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+
+def build_examples(verbose: bool = False) -> list[Path]:
+    """The C callers of the library (examples/*.c): plain gcc against the C ABI and the
+    HIP runtime, linked to the in-tree libtreeverify.so through an $ORIGIN rpath."""
+    built = []
+    for source in sorted(EXAMPLES.glob("*.c")):
+        binary = source.with_suffix("")
+        cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM / 'include'}",
+               f"-I{REPO / 'include'}", str(source), f"-L{OUTPUT.parent}", "-ltreeverify", f"-L{ROCM / 'lib'}",
+               "-lamdhip64", "-lm", "-Wl,-rpath,$ORIGIN/../jetspec_amd", f"-Wl,-rpath,{ROCM / 'lib'}",
+               "-o", str(binary)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        messages = _run(cmd, source.name)
+        if messages:
+            raise RuntimeError(f"{source.name}: compiler warnings:\n" + "\n".join(messages))
+        built.append(binary)
+    return built
 
 
 def main() -> int:
