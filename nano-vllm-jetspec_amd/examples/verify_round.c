@@ -368,5 +368,18 @@ int main(void) {
     printf("verify_round: %d requests, %d tree rows, %d work items; attention max-abs %.2e mean-abs %.2e; "
            "append + commit byte-exact: %s\n", R, total, info.num_items, max_abs, mean_abs, differing ? "no" : "yes");
     printf("verify_round: %s\n", failures ? "FAILED" : "OK");
+
+    void* device_buffers[] = {d_pool, d_new, d_q, d_out, d_bias, d_cu, d_plen, d_cnt, d_tab, d_slots, d_q2r,
+                              d_loc, d_boff, d_words, d_status, d_items, d_groups, d_ws, d_src, d_dst, d_cws};
+    for (size_t i = 0; i < sizeof(device_buffers) / sizeof(device_buffers[0]); ++i)
+        if (device_buffers[i]) CHECK_HIP(hipFree(device_buffers[i]));
+    free(out);
+    free(pool_after);
+    free(items);
+    free(groups);
+    free(q);
+    free(new_kv);
+    free(pool);
+    free(bias);
     return failures ? 1 : 0;
 }
