@@ -128,3 +128,42 @@ def test_large_random_batch_matches_oracle_on_sampled_rows(seed):
     assert torch.isfinite(out).all().item(), label
     assert_within_gate(out, oracle_rows(q, k, v, meta, 128 ** -0.5, picks, rows_per_request=8), label)
     assert read_and_clear_status(q.device) == 0
+
+
+@pytest.mark.parametrize("requests,seed", [(600, 11), (1500, 12)])
+def test_many_requests_match_oracle_on_sampled_rows(requests, seed):
+    """Hundreds of small requests in one launch: thousands of work items, mostly two-head
+    items of short trees, every request's rows at a different packed offset; sampled
+    requests against the fp64 oracle, the whole output finite over a NaN-free pool."""
+    rng = np.random.default_rng(seed)
+    block, kv_heads = 256, 8
+    prefixes = [int(x) for x in rng.integers(0, 2500, size=requests)]
+    counts = [int(rng.choice([1, 2, 9, 16, 32, 33, 64])) for _ in range(requests)]
+    parents = [workloads.random_parents(n, int(rng.integers(1, 8)), rng) for n in counts]
+    prefix_pages = [-(-p // block) for p in prefixes]
+    scratch_pages = -(-sum(counts) // block) + 1
+    total = sum(prefix_pages) + scratch_pages + 1
+    order = rng.permutation(total)
+    tables, cursor = [], 0
+    for n in prefix_pages:
+        tables.append([int(x) for x in order[cursor:cursor + n]])
+        cursor += n
+    scratch = order[cursor:cursor + scratch_pages]
+    pool_slots = (scratch[:, None] * block + np.arange(block)).reshape(-1)[rng.permutation(scratch_pages * block)]
+    slots, off = [], 0
+    for n in counts:
+        slots.append(torch.as_tensor(pool_slots[off:off + n].astype(np.int64), device=DEV))
+        off += n
+    masks = [torch.as_tensor(workloads.ancestor_mask(p), device=DEV) for p in parents]
+    meta = PackedTreeMetadata.build(prefixes, tables, slots, masks, block)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    k = torch.randn((total, block, kv_heads, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    v = torch.randn((total, block, kv_heads, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    q = torch.randn((meta.total_queries, 4 * kv_heads, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    picks = sorted({0, requests - 1} | {int(x) for x in rng.choice(requests, size=4, replace=False)})
+    print(f"[many] R={requests} rows={meta.total_queries} pages={total} checked={picks}", flush=True)
+    out = packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item()
+    assert_within_gate(out, oracle_rows(q, k, v, meta, 128 ** -0.5, picks), f"{requests} requests")
+    assert read_and_clear_status(q.device) == 0
