@@ -57,6 +57,9 @@ def parse_args():
     parser.add_argument("--kv-heads", type=int, default=8, choices=(1, 2, 4, 8),
                         help="KV heads of the batch (4 query heads each); below 8 it is one tensor-parallel "
                              "shard, measured on the verify step only")
+    parser.add_argument("--groups", type=int, default=4, choices=(1, 2, 3, 4, 5, 6, 7, 8, 16),
+                        help="query heads per KV head (4 in the Qwen3-8B geometry; 8 for Qwen3-32B, 16 for "
+                             "Qwen3-235B-A22B); other than 4 it is measured on the verify step only")
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
                              "launches); 'all' adds the rope_scatter, accept and graph legs")
@@ -332,6 +335,8 @@ def run_verify(args, torch):
     kwargs = {} if args.seed is None else {"seed": args.seed}
     if args.kv_heads != 8:
         kwargs["kv_heads"] = args.kv_heads
+    if args.groups != 4:
+        kwargs["groups"] = args.groups
     batch = builder("cuda", **kwargs)
     meta = batch.metadata
     stream = torch.cuda.current_stream()
@@ -397,14 +402,17 @@ def run_verify(args, torch):
                      "peak": MFMA_BF16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
                      "unit": "TFLOP/s" if mfma_bound else "GB/s",
                      "frac": tflops / MFMA_BF16_PEAK_TFLOPS if mfma_bound else achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_bytes(f"cfg{args.config}") if args.kv_heads == 8 else None,
+                     "traffic": (traffic_bytes(f"cfg{args.config}") if args.kv_heads == 8 and args.groups == 4
+                                 else None),
                      "kernel": "tree_attention_kernel", "kernel_ms": attn_ms, "algorithmic_bytes": algo_bytes,
                      "algorithmic_flops": algo_flops, "achieved_gbs": achieved, "achieved_tflops": tflops,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
     }
     if args.kv_heads != 8:
         result["config"]["shard"] = f"tensor-parallel shard: {batch.kv_heads} of 8 KV heads"
-    if args.legs == "all" and args.kv_heads == 8:
+    if args.groups != 4:
+        result["config"]["geometry"] = f"{args.groups} query heads per KV head"
+    if args.legs == "all" and args.kv_heads == 8 and args.groups == 4:
         result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
         result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
@@ -413,7 +421,8 @@ def run_verify(args, torch):
     probe = copy_probe(torch)
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]
-    if args.cpu_requests > 0 and args.config in (1, 2, 4, 5) and args.operands == "normal":
+    if (args.cpu_requests > 0 and args.config in (1, 2, 4, 5) and args.operands == "normal"
+            and args.groups == 4 and args.kv_heads == 8):
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_requests)
     return result
 
