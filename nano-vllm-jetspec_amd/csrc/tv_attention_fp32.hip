@@ -272,13 +272,17 @@ tree_attention_fp32_kernel(const Fp32Params p) {
         __syncthreads();
         kv_load(0);
         if (ntiles > 1) slot_store(TK, slot_load(TK), 1);
+        int64_t next_slot = -1;   // slot of key (t + 1) * TK + tid, loaded during iteration t - 1
         for (int t = 0; t < ntiles; ++t) {
             const int t0 = t * TK;
-            __syncthreads();   // tile t - 1's LDS reads are done; tile t + 1's slots are in LDS
+            __syncthreads();   // every wave is done with tile t - 1 (its K/V rows and its slot buffer)
+            // Tile t + 1's slots go into the buffer tile t - 1 used: only after the barrier, since
+            // every wave reads its tile's slot buffer in its own compute (the visibility test).
+            if (t >= 1 && t + 1 < ntiles) slot_store(t0 + TK, next_slot, (t + 1) & 1);
             kv_store();
-            __syncthreads();   // tile t is staged
+            __syncthreads();   // tile t is staged; tile t + 1's slots are in LDS
             if (t + 1 < ntiles) kv_load((t + 1) & 1);
-            const int64_t next_slot = t + 2 < ntiles ? slot_load(t0 + 2 * TK) : -1;
+            next_slot = t + 2 < ntiles ? slot_load(t0 + 2 * TK) : -1;
             if (row_ok) {
                 const int pos = t0 + lane;
                 bool visible = lane < TK && pos < my_end && kbase_lds[t & 1][lane < TK ? lane : 0] >= 0;
@@ -345,8 +349,6 @@ tree_attention_fp32_kernel(const Fp32Params p) {
                     }
                 }
             }
-            // Tile t's slot buffer was read by the loads issued in the previous iteration.
-            if (t + 2 < ntiles) slot_store(t0 + 2 * TK, next_slot, t & 1);
         }
         if (row_ok) {
 #pragma unroll
