@@ -291,6 +291,37 @@ def test_plan_chunks_fit_the_page_cache(block):
             assert max(spans) >= MAX_CHUNK_PAGES - 1, "the page cap binds when each unit has long work"
 
 
+def _slot_plan_items(prefix, nodes, kv_heads, groups, cus):
+    lib = _lib.library()
+    prefixes, counts, info = (ctypes.c_int32 * 1)(prefix), (ctypes.c_int32 * 1)(nodes), _lib.PlanInfo()
+    _lib.check(lib.tv_tree_attention_plan_slots(prefixes, counts, 1, kv_heads, groups, cus, 0, None, None,
+                                                ctypes.byref(info)), "plan_slots")
+    items = np.zeros((max(info.num_items, 1), 8), dtype=np.int32)
+    merges = np.zeros((max(info.num_groups, 1), 8), dtype=np.int32)
+    _lib.check(lib.tv_tree_attention_plan_slots(prefixes, counts, 1, kv_heads, groups, cus, 0,
+                                                items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                                merges.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                                ctypes.byref(info)), "plan_slots")
+    return items[:info.num_items]
+
+
+@pytest.mark.parametrize("prefix,nodes,kv_heads,groups,same", [
+    (5000, 16, 2, 4, True), (9000, 64, 2, 4, True), (9000, 200, 8, 16, False), (5000, 1024, 8, 8, False)])
+def test_slot_plan_caps_prefix_chunks(prefix, nodes, kv_heads, groups, same):
+    """The slot-addressed plan (the legacy entry) caches at most 2048 prefix slots per item;
+    the page plan's cap is 511 pages.  Where the page plan would give a chunk longer than
+    2048 keys (few, long work items: one request with many heads and nodes) the two split the
+    prefix differently, so the legacy entry then equals the packed exact entry only within
+    rounding, not byte for byte; elsewhere the two plans are the same item for item."""
+    slot_items = _slot_plan_items(prefix, nodes, kv_heads, groups, 256)
+    assert int((slot_items[:, 4] - slot_items[:, 3]).max()) <= 2048
+    page_items = make_plan([prefix], [nodes], kv_heads, 256, 256, queries_per_kv=groups)["items"]
+    key = lambda items: sorted(map(tuple, items[:, :5].tolist()))
+    assert (key(slot_items) == key(page_items)) == same
+    if not same:
+        assert int((page_items[:, 4] - page_items[:, 3]).max()) > 2048
+
+
 def test_plan_at_benchmark_shapes():
     rng = np.random.default_rng(4)
     prefixes = [int(x) for x in rng.integers(8192, 32769, size=64)]

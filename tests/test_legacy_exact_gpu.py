@@ -2,10 +2,11 @@
 
 * paged_tree_attention (paged_backend.py:309-415) as the legacy c1 path calls it
   (models/qwen3.py:270-302): the pool viewed as 16-token sub-pages, a logical slot per key
-  (prefix through the page table, then the tree's scratch slots) and a 0 / -inf bias.  It
-  must equal the packed FP32 entry on the same request byte for byte (the reference's
-  "packed == per-request legacy" test, tests/test_jetspec_packed_attention.py:156-188) and
-  meet the gate against the fp64 oracle.
+  (prefix through the page table, then the tree's scratch slots) and a 0 / -inf bias.  Where
+  its plan splits the prefix as the page plan does, it must equal the packed exact entry on
+  the same request byte for byte (the reference's "packed == per-request legacy" test,
+  tests/test_jetspec_packed_attention.py:156-188); it must always meet the gate against the
+  fp64 oracle.
 * The FP32 entries keep probabilities exact: their FP32 output meets the reference's FP32
   qualification bound (FP32_ATTENTION_BOUND = 1e-4 on max-abs and relative RMS,
   benchmarks/jetspec_numeric_oracles.py:21,108-168) against the fp64 oracle, which the
@@ -62,6 +63,22 @@ def test_legacy_c1_equals_packed_fp32_entry_bytewise(prefixes, counts):
         full = torch.zeros_like(q)
         full[rows] = legacy
         assert_within_gate(full, {r: expect[r]}, f"legacy c1 request {r} (P={meta.prefix_lengths[r]})")
+    assert read_and_clear_status(DEV) == 0
+
+
+def test_legacy_long_prefix_with_differently_split_plans_meets_the_gate():
+    """One request with a long prefix, 8 KV heads x 16 query heads and 200 nodes: the page plan
+    splits the prefix into chunks above the 2048 slots a slot-addressed item caches, so the
+    legacy entry's plan splits it finer and its split-K merges round differently.  The result
+    then stays within the gate of the fp64 oracle and within bf16 rounding of the packed entry."""
+    q, k, v, meta, slots, masks, _ = reference_fixture(prefixes=(9000,), counts=(200,), kv_heads=8, groups=16)
+    legacy = legacy_call(q, k, v, 9000, meta.block_tables_host[0], slots[0], masks[0])
+    packed = packed_tree_attention_reference(q, k, v, meta, SCALE, 16)
+    torch.cuda.synchronize()
+    assert torch.isfinite(legacy.float()).all().item(), "NaN padding was read"
+    assert (legacy.float() - packed.float()).abs().max().item() < 2e-3
+    assert_within_gate(legacy, oracle_rows(q, k, v, meta, SCALE, [0], rows_per_request=16),
+                       "legacy c1 P=9000 T=200 kv=8 G=16")
     assert read_and_clear_status(DEV) == 0
 
 
