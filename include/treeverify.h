@@ -108,7 +108,10 @@ int tv_store_kvcache(const void* key, int64_t key_row_stride,
  *     pool[kv, l, dst[i] / B, dst[i] % B] = pool[kv, l, src[i] / B, src[i] % B]
  * with the reference's gather-then-scatter semantics: if any destination slot is
  * also a source slot, all sources are read before any destination is written
- * (through `workspace`), otherwise the rows are copied directly.
+ * (through `workspace`), otherwise the rows are copied directly.  Destination
+ * slots must be distinct: which source lands in a repeated destination is
+ * unspecified, as in the reference's indexed assignment on the GPU.  Sources
+ * may repeat.
  * workspace must hold tv_copy_accepted_kv_workspace_bytes(...) bytes.
  * On success *payload_bytes (host, may be NULL) receives 2*L*num_slots*H*D*elem,
  * the reference's return value.

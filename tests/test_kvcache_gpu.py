@@ -83,9 +83,8 @@ def small_commit_case(seed, overlap=False, layers=4, rows=200, pages=12):
     return pool, src.astype(np.int64), dst.astype(np.int64)
 
 
-# 200 rows take the one-launch commit; 3000 rows (above its 2048-slot limit) the
-# check + move launches.
-@pytest.mark.parametrize("rows,layers,pages", [(200, 4, 12), (3000, 2, 24)])
+# Up to 512 rows take the one-launch commit; 513 and 3000 rows the check + move launches.
+@pytest.mark.parametrize("rows,layers,pages", [(200, 4, 12), (512, 2, 12), (513, 2, 12), (3000, 2, 24)])
 @pytest.mark.parametrize("overlap", [False, True])
 def test_commit_bit_exact_against_oracle(overlap, rows, layers, pages):
     pool, src, dst = small_commit_case(11, overlap, layers=layers, rows=rows, pages=pages)
