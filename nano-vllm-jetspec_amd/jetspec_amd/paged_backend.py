@@ -12,7 +12,7 @@ relative (two MFMAs: its rounding and the rounding of the remainder) and sum it 
 fp32, the reference's "never BF16 probabilities" (paged_backend.py:248-256).
 
 Batches outside the MFMA kernel's geometry (f32 operands, head sizes other than 128,
-query groups other than 1/2/4/8/16, page sizes that are not multiples of 32, trees
+query groups other than 1-8 and 16, page sizes that are not multiples of 32, trees
 above 1024 nodes, unaligned pools) run the FP32 kernel (tv_tree_attention_fp32), as the
 reference's dispatcher runs its scalar FP32 kernel outside its fast kernel's geometry
 (paged_backend.py:288-306).  It reads every metadata value from device memory, needs
