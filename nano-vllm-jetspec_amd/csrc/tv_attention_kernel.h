@@ -644,7 +644,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // offset; a new page is read from the LDS page list, prefetched one page ahead,
     // when the current one is used up.  Pages hold whole tiles when B is a multiple
     // of the tile (the item's first key is).
-    const int t_fast = (B % kTileKeys == 0 && !slot_mode && !EXACT) ? max(0, nfull - (NS - 2)) : 0;
+    const int t_fast = (B % kTileKeys == 0 && !slot_mode) ? max(0, nfull - (NS - 2)) : 0;
     uint64_t fk = 0, fv = 0;     // K and V base of the next streamed tile (head h0)
     int f_left = 0, f_pidx = 0;  // tiles left in its page; the page's index in `pages`
     int32_t f_next = 0;          // page number at f_pidx + 1
@@ -705,16 +705,22 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         raise_max(s, true);
     }
     // Fast steps.  Active waves alternate two register sets for the scores and the
-    // probabilities by tile parity (NS is even, so the parity of t is that of b), so no
-    // copies between steps; inactive waves only stage their share of the tiles.  (EXACT
-    // items run every step in the general loop.)
-    if constexpr (!EXACT) {
+    // probabilities (and, for EXACT, the probabilities' remainders) by tile parity (NS is
+    // even, so the parity of t is that of b), so no copies between steps; inactive waves
+    // only stage their share of the tiles.
     if (wave_active) {
         f32x16 sc[2];
-        V8 pp[2][2];
+        V8 pp[2][2], pq[2][2];
+        auto& pr_sets = [&]() -> V8 (&)[2][2] {
+            if constexpr (EXACT) return pq; else return pp;
+        }();
         sc[0] = s;
         pp[0][0] = pb_prev[0];
         pp[0][1] = pb_prev[1];
+        if constexpr (EXACT) {
+            pq[0][0] = pl_prev[0];
+            pq[0][1] = pl_prev[1];
+        }
         for (int t0 = 0; t0 < t_fast; t0 += NS) {
 #pragma unroll
             for (int b = 0; b < NS; ++b) {
@@ -734,12 +740,13 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     if (sl == 12) fast_advance();
                 };
                 f32x16& s_cur = sc[b & 1];
-                float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1],
-                                ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET, piece);
+                float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], pr_sets[b & 1],
+                                pr_sets[(b + 1) & 1], ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET,
+                                piece);
                 const bool need = !(lt <= kMaxTileSum);
                 if (__any(need)) {
                     raise_max(s_cur, need);
-                    lt = probabilities(s_cur, pp[(b + 1) & 1], pp[(b + 1) & 1]);
+                    lt = probabilities(s_cur, pp[(b + 1) & 1], pr_sets[(b + 1) & 1]);
                 }
                 l_run += lt;
             }
@@ -748,6 +755,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         s = odd ? sc[1] : sc[0];
         pb_prev[0] = odd ? pp[1][0] : pp[0][0];
         pb_prev[1] = odd ? pp[1][1] : pp[0][1];
+        if constexpr (EXACT) {
+            pl_prev[0] = odd ? pq[1][0] : pq[0][0];
+            pl_prev[1] = odd ? pq[1][1] : pq[0][1];
+        }
     } else {
         for (int t0 = 0; t0 < t_fast; t0 += NS) {
 #pragma unroll
@@ -764,7 +775,6 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 fast_advance();
             }
         }
-    }
     }
     // The remaining steps: masks, partial and tree tiles, general DMA.
     int pf = fetch(t_fast + NS - 2);
