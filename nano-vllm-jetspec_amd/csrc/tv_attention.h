@@ -45,6 +45,7 @@ struct AttnParams {
     const int32_t* counts;   // device {items, groups, ...} of a device-built plan, or null
     float* ws_o;
     float2* ws_ml;
+    int32_t num_slots;       // partial-result slots the workspace holds (items' and groups' slot bound)
     int32_t* status;
     int32_t qpk;             // query heads per KV head (G; the merge kernel reads it)
 };

@@ -23,7 +23,11 @@ template <typename T>
 __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     const int32_t* gr = p.groups + 8 * static_cast<int64_t>(group);
     const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
-    if (r < 0 || r >= p.num_requests) return;
+    if (r < 0 || r >= p.num_requests || h0 < 0 || n0 < 0 || (hpw != 1 && hpw != 2) || first < 0 || ns < 1 ||
+        first > p.num_slots - ns) {
+        if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+        return;
+    }
     const int wph = 8 / hpw;
     const int G = p.qpk, nw = 32 / G;   // query heads per KV head, nodes per wave (floor)
     const int wr = 8 * blockIdx.y + (threadIdx.x >> 5), quad = threadIdx.x & 31;
@@ -221,7 +225,8 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     if ((a->out_stride_row | a->out_stride_head) % (16 / out_elem) || !aligned(a->out, 16)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: output rows must be 16-byte aligned");
     }
-    if (a->num_requests < 1 || a->total_queries < 0 || a->num_items < 0 || a->num_groups < 0) {
+    if (a->num_requests < 1 || a->total_queries < 0 || a->num_items < 0 || a->num_groups < 0 ||
+        a->num_partial_slots < 0) {
         return fail(TV_ERR_INVALID, "tree_attention: invalid counts");
     }
     // Tree slots are cached as 32-bit values.
@@ -237,7 +242,7 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     const int64_t o_bytes = static_cast<int64_t>(a->num_partial_slots) * kRowsPerItem * kHeadDim * 4;
     const int64_t o_span = (o_bytes + 255) / 256 * 256;
     const int64_t need = a->num_partial_slots ? o_span + (static_cast<int64_t>(a->num_partial_slots) * kRowsPerItem * 8 + 255) / 256 * 256 : 0;
-    if (a->num_groups > 0 && (!a->groups || !a->workspace)) {
+    if ((a->num_groups > 0 && !a->groups) || (a->num_partial_slots > 0 && !a->workspace)) {
         return fail(TV_ERR_INVALID, "tree_attention: split plan without groups/workspace");
     }
     if (a->workspace_bytes < need) {
@@ -282,6 +287,7 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     p.counts = a->device_counts;
     p.ws_o = static_cast<float*>(a->workspace);
     p.ws_ml = a->workspace ? reinterpret_cast<float2*>(static_cast<char*>(a->workspace) + o_span) : nullptr;
+    p.num_slots = a->workspace ? a->num_partial_slots : 0;
     p.status = a->status;
     hipStream_t s = as_stream(stream);
     const bool exact = a->exact_probabilities != 0;

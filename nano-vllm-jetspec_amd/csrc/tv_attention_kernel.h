@@ -188,7 +188,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const int head = it.h0 + hl;
     const int nsub = wave - hl * WPH;
     const int r = it.r;
-    const int tn = p.cnt[r], qbase = p.cu[r];
+    const int tn = p.cnt[r], qbase = p.cu[r], plen = p.plen[r];
     const int node = it.n0 + NW * nsub + c / G;
     const int qh = head * G + c % G;
     const bool head_ok = head < p.num_kv_heads;
@@ -205,8 +205,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const int page0 = it.kbeg / B;
     const int nkeys = it.kend - it.kbeg;
     const int npages = slot_mode ? 0 : (nkeys > 0 ? (it.kend - 1) / B - page0 + 1 : 0);
-    // The planner keeps every item within the LDS page/slot caches and non-empty.
-    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk)) {
+    // The planner keeps every item within the LDS page/slot caches, non-empty, inside its
+    // request's prefix and inside the workspace; an item that is not (a plan made for other
+    // metadata) is reported and skipped rather than read past the request's table row.
+    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk) ||
+        it.h0 < 0 || it.n0 < 0 || it.kbeg < 0 || it.kend < it.kbeg || it.kend > plen || it.slot >= p.num_slots) {
         if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
     }

@@ -136,6 +136,15 @@ def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
     big.num_blocks, big.num_requests = (1 << 31) // 256, 1
     assert lib.tv_tree_attention(ctypes.byref(big), None) == _lib.TV_ERR_UNSUPPORTED
     assert b"at most 2^31 slots" in lib.tv_last_error()
+    # A split plan's partial slots need a workspace; a negative slot count is invalid.
+    for slots, workspace, message in ((-1, 0x20000, b"invalid counts"), (4, 0, b"without groups/workspace")):
+        a = args((256 * 256, 256, 128, 1))
+        a.num_blocks, a.num_requests, a.num_items = 8, 1, 1
+        a.cu_seqlens_q = a.prefix_lens = a.node_counts = a.block_tables = a.items = 0x10000
+        a.tree_slots = a.ancestor_words = 0x10000
+        a.num_partial_slots, a.workspace, a.workspace_bytes = slots, workspace, 1 << 30
+        assert lib.tv_tree_attention(ctypes.byref(a), None) == _lib.TV_ERR_INVALID, slots
+        assert message in lib.tv_last_error()
 
 
 def nodes_per_item(hpw, groups):
