@@ -40,7 +40,16 @@ __device__ __forceinline__ float elem_value(const float* p, int64_t i) { return 
 // visits its elements in increasing index order, so within a thread a later element
 // replaces the best one only if it is larger, or a NaN replacing a number: equal
 // values and later NaNs keep the earlier index.  Four loads are issued per iteration
-// so that each wave keeps several in flight.
+// so that each wave keeps several in flight.  The logits are read once, so the vector
+// loads are non-temporal (0.210 -> 0.185 ms for 4096 x 151936 bf16 rows, 5.9 -> 6.7 TB/s).
+//
+// The vector scan tracks units, not elements: per unit only its maximum and whether it
+// holds a NaN, and a unit replaces the thread's best unit when its maximum is larger,
+// or when it holds a NaN and the best unit does not (the first such unit, since a later
+// unit must beat it strictly).  The best unit's raw bits are kept, and at the end its
+// elements are visited in order, which gives the first element of the thread's largest
+// value (or its first NaN): the element an element-by-element scan keeps, with about a
+// third of its VALU work per element (0.225 -> 0.210 ms on the same rows).
 template <typename S, int VEC>
 __global__ void __launch_bounds__(kArgmaxThreads)
 argmax_rows_kernel(const S* __restrict__ logits, int64_t row_stride, int64_t vocab, int64_t* __restrict__ out) {
@@ -60,12 +69,15 @@ argmax_rows_kernel(const S* __restrict__ logits, int64_t row_stride, int64_t voc
     const int64_t units = VEC > 1 ? vocab / VEC : 0;
     if constexpr (VEC > 1) {
         static_assert(VEC * sizeof(S) == sizeof(u32x4), "a vector unit is one 16-byte load");
+        float unit_max = -INFINITY;   // the best unit's maximum (NaN once a unit holding a NaN is taken)
+        int64_t unit = -1;            // the best unit
+        u32x4 unit_raw = {0u, 0u, 0u, 0u};
         for (int64_t u0 = threadIdx.x; u0 < units; u0 += kUnroll * kArgmaxThreads) {
             u32x4 raw[kUnroll];
 #pragma unroll
             for (int k = 0; k < kUnroll; ++k) {
                 const int64_t u = u0 + k * kArgmaxThreads;
-                if (u < units) raw[k] = *reinterpret_cast<const u32x4*>(base + u * VEC);
+                if (u < units) raw[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + u * VEC));
             }
 #pragma unroll
             for (int k = 0; k < kUnroll; ++k) {
@@ -73,10 +85,23 @@ argmax_rows_kernel(const S* __restrict__ logits, int64_t row_stride, int64_t voc
                 if (u < units) {
                     S vals[VEC];
                     __builtin_memcpy(vals, &raw[k], sizeof(vals));
+                    // NaN-propagating maximum (v_maximum3_f32): NaN when the unit holds one.
+                    // Its -0 < +0 order is harmless: the maximum is only compared with > and ==.
+                    float m = elem_value(vals, 0);
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) visit(elem_value(vals, e), u * VEC + e);
+                    for (int e = 1; e < VEC; ++e) m = __builtin_elementwise_maximum(m, elem_value(vals, e));
+                    const bool take = unit < 0 || m > unit_max || (m != m && unit_max == unit_max);
+                    unit_max = take ? m : unit_max;
+                    unit = take ? u : unit;
+                    unit_raw = take ? raw[k] : unit_raw;
                 }
             }
+        }
+        if (unit >= 0) {
+            S vals[VEC];
+            __builtin_memcpy(vals, &unit_raw, sizeof(vals));
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) visit(elem_value(vals, e), unit * VEC + e);
         }
     }
     for (int64_t i = units * VEC + threadIdx.x; i < vocab; i += kArgmaxThreads) visit(elem_value(base, i), i);
