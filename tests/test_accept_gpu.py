@@ -39,7 +39,7 @@ def test_argmax_equals_torch(dtype, rows, vocab):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_argmax_edge_rows(dtype):
     vocab = 3001
-    logits = torch.randn(12, vocab, device=DEV).to(dtype)
+    logits = torch.randn(18, vocab, device=DEV).to(dtype)
     logits[0] = 1.5                                        # all equal -> 0
     logits[1] = float("-inf")                              # all -inf -> 0
     logits[2, 17] = logits[2, 2000] = 1e4                  # tie -> lower index
@@ -56,6 +56,16 @@ def test_argmax_edge_rows(dtype):
     logits[10] = float("-inf")
     logits[10, 1234] = -3e38 if dtype == torch.float32 else -3.0e38
     logits[11, ::2] = 2.0                                  # many ties
+    # The scan keeps one 16-byte unit per thread (8 bf16 or 4 fp32 elements) and resolves
+    # the element inside it at the end: NaN and ties inside and across units.
+    logits[12, 16], logits[12, 17] = 1e4, float("nan")     # NaN after the max in one unit
+    logits[13, 24], logits[13, 25] = float("nan"), 1e4     # NaN before the max in one unit
+    logits[14, 40], logits[14, 2500] = 1e4, float("nan")   # a later unit's NaN beats an earlier max
+    logits[15] = -1.0
+    logits[15, 8], logits[15, 800] = -0.0, 0.0             # -0 then +0: equal, the first wins
+    logits[16] = -1.0
+    logits[16, 8], logits[16, 800] = 0.0, -0.0             # +0 then -0
+    logits[17, 15] = logits[17, 16] = 5e3                  # equal maxima in adjacent units
     got = greedy_argmax(logits)
     assert torch.equal(got, logits.argmax(-1))
 
