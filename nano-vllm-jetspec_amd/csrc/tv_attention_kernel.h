@@ -122,6 +122,17 @@ __device__ __forceinline__ void dma_b128_s(uint32_t lane_offset, const void* bas
                  : "s"(lds_addr), "v"(lane_offset), "s"(base)
                  : "memory", "m0");
 }
+__device__ __forceinline__ void dma_b128_s_nt(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+                 :
+                 : "s"(lds_addr), "v"(lane_offset), "s"(base)
+                 : "memory", "m0");
+}
+// Compile-time choice of the streaming DMA's cache policy (non-temporal or not).
+template <bool B>
+struct NtTag {
+    static constexpr bool value = B;
+};
 __device__ __forceinline__ void dma_b32_s(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                  :
@@ -671,12 +682,21 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         fv = v_head_u + static_cast<uint64_t>(page) * v_page_b + static_cast<uint64_t>(off0) * v_key_b;
         f_next = pages[min(f_pidx + 1, npages - 1)];
     }
-    auto fast_issue_k = [&](int stage, int j) {
-        dma_b128_s(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * kTileBytes));
+    auto fast_issue_k = [&](auto nt, int stage, int j) {
+        if constexpr (decltype(nt)::value) {
+            dma_b128_s_nt(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * kTileBytes));
+        } else {
+            dma_b128_s(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * kTileBytes));
+        }
     };
-    auto fast_issue_v = [&](int stage, int j) {
-        dma_b128_s(v_lane_h[j], reinterpret_cast<const void*>(fv),
-                   tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+    auto fast_issue_v = [&](auto nt, int stage, int j) {
+        if constexpr (decltype(nt)::value) {
+            dma_b128_s_nt(v_lane_h[j], reinterpret_cast<const void*>(fv),
+                          tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+        } else {
+            dma_b128_s(v_lane_h[j], reinterpret_cast<const void*>(fv),
+                       tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+        }
     };
     auto fast_advance = [&]() {
         fk += k_tile_b;
@@ -711,73 +731,86 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // probabilities (and, for EXACT, the probabilities' remainders) by tile parity (NS is
     // even, so the parity of t is that of b), so no copies between steps; inactive waves
     // only stage their share of the tiles.
-    if (wave_active) {
-        f32x16 sc[2];
-        V8 pp[2][2], pq[2][2];
-        auto& pr_sets = [&]() -> V8 (&)[2][2] {
-            if constexpr (EXACT) return pq; else return pp;
-        }();
-        sc[0] = s;
-        pp[0][0] = pb_prev[0];
-        pp[0][1] = pb_prev[1];
-        if constexpr (EXACT) {
-            pq[0][0] = pl_prev[0];
-            pq[0][1] = pl_prev[1];
-        }
-        for (int t0 = 0; t0 < t_fast; t0 += NS) {
+    // Long streams that no other item reads (the request's tree fits one node block, and at
+    // least 64 streamed tiles) use non-temporal loads: 2 % faster on the long-context batches,
+    // whose K/V is read once.  Streams shared with other node blocks stay cacheable in L2
+    // for them (non-temporal loads made those 4 % slower), and short streams, which are
+    // latency-bound, measured slightly slower non-temporal too.  The exact instance keeps one
+    // form (a second one would not fit its registers).
+    auto fast_steps = [&](auto nt) {
+        if (wave_active) {
+            f32x16 sc[2];
+            V8 pp[2][2], pq[2][2];
+            auto& pr_sets = [&]() -> V8 (&)[2][2] {
+                if constexpr (EXACT) return pq; else return pp;
+            }();
+            sc[0] = s;
+            pp[0][0] = pb_prev[0];
+            pp[0][1] = pb_prev[1];
+            if constexpr (EXACT) {
+                pq[0][0] = pl_prev[0];
+                pq[0][1] = pl_prev[1];
+            }
+            for (int t0 = 0; t0 < t_fast; t0 += NS) {
 #pragma unroll
-            for (int b = 0; b < NS; ++b) {
-                const int t = t0 + b;
-                if (t >= t_fast) break;
-                wait_vmcnt<(NS - 4) * LPT>();
-                __syncthreads();
-                const int ds = (b + NS - 2) % NS;
-                auto piece = [&](int sl) {
-                    if (HPW == 1) {
-                        if (sl == 4) fast_issue_k(ds, 0);
-                        if (sl == 8) fast_issue_v(ds, 0);
-                    } else {
-                        if (sl == 3 || sl == 5) fast_issue_k(ds, (sl - 3) >> 1);
-                        if (sl == 7 || sl == 9) fast_issue_v(ds, (sl - 7) >> 1);
+                for (int b = 0; b < NS; ++b) {
+                    const int t = t0 + b;
+                    if (t >= t_fast) break;
+                    wait_vmcnt<(NS - 4) * LPT>();
+                    __syncthreads();
+                    const int ds = (b + NS - 2) % NS;
+                    auto piece = [&](int sl) {
+                        if (HPW == 1) {
+                            if (sl == 4) fast_issue_k(nt, ds, 0);
+                            if (sl == 8) fast_issue_v(nt, ds, 0);
+                        } else {
+                            if (sl == 3 || sl == 5) fast_issue_k(nt, ds, (sl - 3) >> 1);
+                            if (sl == 7 || sl == 9) fast_issue_v(nt, ds, (sl - 7) >> 1);
+                        }
+                        if (sl == 12) fast_advance();
+                    };
+                    f32x16& s_cur = sc[b & 1];
+                    float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], pr_sets[b & 1],
+                                    pr_sets[(b + 1) & 1], ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET,
+                                    piece);
+                    const bool need = !(lt <= kMaxTileSum);
+                    if (__any(need)) {
+                        raise_max(s_cur, need);
+                        lt = probabilities(s_cur, pp[(b + 1) & 1], pr_sets[(b + 1) & 1]);
                     }
-                    if (sl == 12) fast_advance();
-                };
-                f32x16& s_cur = sc[b & 1];
-                float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], pr_sets[b & 1],
-                                pr_sets[(b + 1) & 1], ((b + 1) % NS) * TILE_SET, ((b + NS - 1) % NS) * TILE_SET,
-                                piece);
-                const bool need = !(lt <= kMaxTileSum);
-                if (__any(need)) {
-                    raise_max(s_cur, need);
-                    lt = probabilities(s_cur, pp[(b + 1) & 1], pr_sets[(b + 1) & 1]);
+                    l_run += lt;
                 }
-                l_run += lt;
+            }
+            const bool odd = t_fast & 1;
+            s = odd ? sc[1] : sc[0];
+            pb_prev[0] = odd ? pp[1][0] : pp[0][0];
+            pb_prev[1] = odd ? pp[1][1] : pp[0][1];
+            if constexpr (EXACT) {
+                pl_prev[0] = odd ? pq[1][0] : pq[0][0];
+                pl_prev[1] = odd ? pq[1][1] : pq[0][1];
+            }
+        } else {
+            for (int t0 = 0; t0 < t_fast; t0 += NS) {
+#pragma unroll
+                for (int b = 0; b < NS; ++b) {
+                    const int t = t0 + b;
+                    if (t >= t_fast) break;
+                    wait_vmcnt<(NS - 4) * LPT>();
+                    __syncthreads();
+                    const int ds = (b + NS - 2) % NS;
+#pragma unroll
+                    for (int j = 0; j < HPW; ++j) fast_issue_k(nt, ds, j);
+#pragma unroll
+                    for (int j = 0; j < HPW; ++j) fast_issue_v(nt, ds, j);
+                    fast_advance();
+                }
             }
         }
-        const bool odd = t_fast & 1;
-        s = odd ? sc[1] : sc[0];
-        pb_prev[0] = odd ? pp[1][0] : pp[0][0];
-        pb_prev[1] = odd ? pp[1][1] : pp[0][1];
-        if constexpr (EXACT) {
-            pl_prev[0] = odd ? pq[1][0] : pq[0][0];
-            pl_prev[1] = odd ? pq[1][1] : pq[0][1];
-        }
+    };
+    if (!EXACT && tn <= NPW && t_fast >= 64) {
+        fast_steps(NtTag<!EXACT>{});
     } else {
-        for (int t0 = 0; t0 < t_fast; t0 += NS) {
-#pragma unroll
-            for (int b = 0; b < NS; ++b) {
-                const int t = t0 + b;
-                if (t >= t_fast) break;
-                wait_vmcnt<(NS - 4) * LPT>();
-                __syncthreads();
-                const int ds = (b + NS - 2) % NS;
-#pragma unroll
-                for (int j = 0; j < HPW; ++j) fast_issue_k(ds, j);
-#pragma unroll
-                for (int j = 0; j < HPW; ++j) fast_issue_v(ds, j);
-                fast_advance();
-            }
-        }
+        fast_steps(NtTag<false>{});
     }
     // The remaining steps: masks, partial and tree tiles, general DMA.
     int pf = fetch(t_fast + NS - 2);
