@@ -62,7 +62,7 @@ def parse_args():
                              "Qwen3-235B-A22B); other than 4 it is measured on the verify step only")
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
-                             "launches); 'all' adds the rope_scatter, accept and graph legs")
+                             "launches); 'all' adds the rope_scatter, accept, graph and exact legs")
     parser.add_argument("--operands", choices=("normal", "constant", "zero", "zero-q", "zero-kv"), default="normal",
                         help="diagnostic: replace the N(0,1) Q/K/V values by constants or zeros (same shapes, "
                              "pages, trees, instructions and bytes) to show the part's data-dependent clock; "
@@ -311,6 +311,34 @@ def graph_leg(batch, torch, steps: int, warmup: int, layers: int = 36) -> dict:
             "speedup": eager_ms / replay_ms, "bitwise_equal": same}
 
 
+def exact_leg(batch, torch, steps: int, warmup: int) -> dict:
+    """The explicit FP32-probability entry (backend="reference", paged_backend.py:248-256) on the
+    same batch: probabilities kept to ~2^-17 relative in the P.V product (two MFMAs per P.V
+    step), HIP events on the launch stream."""
+    from jetspec_amd import packed_tree_attention
+
+    meta, stream = batch.metadata, torch.cuda.current_stream()
+
+    def call():
+        return packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, batch.groups,
+                                     backend="reference")
+    for _ in range(warmup):
+        call()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for e in events:
+        e[0].record(stream)
+        call()
+        e[1].record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    algo = batch.algorithmic_bytes()
+    gbs = algo / (ms * 1e-3) / 1e9
+    return {"kernel": "tree_attention_kernel (exact probabilities)", "backend": "reference", "ms": ms,
+            "algorithmic_bytes": algo, "achieved": gbs, "unit": "GB/s", "peak": HBM_PEAK_GBS,
+            "frac": gbs / HBM_PEAK_GBS}
+
+
 def sustain_leg(batch, torch, seconds: float) -> dict:
     """The verify attention back to back for `seconds` of wall time, synchronising every 50
     launches (a steady load for reading the part's power and clock telemetry)."""
@@ -416,6 +444,7 @@ def run_verify(args, torch):
         result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
         result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
+        result["exact"] = exact_leg(batch, torch, args.steps, args.warmup)
     if args.sustain > 0:
         result["sustained"] = sustain_leg(batch, torch, args.sustain)
     probe = copy_probe(torch)
