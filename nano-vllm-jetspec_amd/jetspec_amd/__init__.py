@@ -7,6 +7,7 @@ Drop-in operators (same names, arguments and errors as the reference):
   PackedTreeMetadata      speculative/jetspec/packed_metadata.py:16-237
   accept_batch            speculative/jetspec/serving_ops.py:55-90
   rope_scatter(_prevalidated)  speculative/jetspec/tree_fusion.py:167-199
+  offset_causal_mask      speculative/jetspec/prefill.py:14-26 (a chunk is a chain tree)
 Each device operator is a hand-written gfx950 HIP kernel in libtreeverify.so.
 """
 from .packed_metadata import PackedTreeMetadata
@@ -22,6 +23,7 @@ from .tree_prefix import (
 )
 from .attention import store_kvcache
 from .tree_fusion import rope_scatter, rope_scatter_prevalidated
+from .prefill import chain_tree_masks, offset_causal_mask
 from .state import commit_slots, copy_accepted_kv, _slots_for_blocks
 from .serving_ops import (accept_batch, accept_batch_device, accept_walk, build_child_maps, greedy_argmax,
                           truncate_accepted)
@@ -43,6 +45,8 @@ __all__ = [
     "store_kvcache",
     "rope_scatter",
     "rope_scatter_prevalidated",
+    "offset_causal_mask",
+    "chain_tree_masks",
     "copy_accepted_kv",
     "commit_slots",
     "accept_batch",
