@@ -64,8 +64,11 @@ enum tv_status_bits {
     TV_STATUS_BAD_REQUEST = 4,  /* metadata row that names a nonexistent request */
     TV_STATUS_BAD_POSITION = 8, /* a RoPE position outside the cos/sin cache */
     TV_STATUS_BAD_DEPTH = 16,   /* an accepted path node off its canonical depth */
-    TV_STATUS_BAD_BIAS = 32     /* a qq_bias entry other than 0 / -inf packed into visibility
+    TV_STATUS_BAD_BIAS = 32,    /* a qq_bias entry other than 0 / -inf packed into visibility
                                    bits (finite values need tv_tree_attention_fp32) */
+    TV_STATUS_STALE_PLAN = 64   /* an attention plan that no longer matches the live metadata:
+                                   a request's prefix length or node count changed after the
+                                   plan was made (tv_tree_attention_plan reads host copies) */
 };
 
 /* ABI version of the loaded library (TV_ABI_VERSION at build time). */
@@ -263,6 +266,17 @@ int tv_truncate_accepted(const int32_t* paths, int32_t path_stride, const int32_
  *   chunk_keys: 0 = automatic; > 0 forces every prefix chunk to that many keys
  *               (a multiple of 32), which makes per-request results independent
  *               of the rest of the batch.
+ * An item is 8 int32: request, first KV head, first node, prefix key begin, key end,
+ * flags, partial-result slot (-1: unsplit), KV heads per item.  Flags: bit 0 = last
+ * prefix chunk (that item also covers the tree), bit 1 = last node block of its
+ * request, bits 8-15 = queries_per_kv.  tv_tree_attention checks every item against the
+ * live device metadata: an item outside its request's prefix, or made for another
+ * queries_per_kv, sets TV_STATUS_BAD_REQUEST and is skipped; a last chunk that ends
+ * before the live prefix length, or a last node block that ends before the live node
+ * count, sets TV_STATUS_STALE_PLAN (the plan's keys and rows are computed, the rest of
+ * the grown request is not).  A merge group is 8 int32: request, first KV head, first
+ * node, KV heads per item, first partial slot, partial count, queries_per_kv, 0; a group
+ * made for another queries_per_kv sets TV_STATUS_BAD_REQUEST and writes nothing.
  */
 typedef struct tv_attention_plan_info {
     int32_t num_items;
@@ -525,6 +539,9 @@ int64_t tv_sizeof_tree_attention_fp32_args(void);
  * the process ends.  A plan whose partial slots need more returns TV_ERR_CAPACITY and
  * launches nothing.  Every call on one device shares that device's scratch, so calls that
  * overlap on one device (concurrent streams) race; calls ordered on one stream do not.
+ * The scratch is the one of the device that `stream` belongs to; its address is looked up
+ * (hipGetSymbolAddress, with that device current) on the first call for that device, which
+ * may happen under graph capture.
  * No hipMalloc, hipFree or allocating library routine is called.
  */
 int tv_tree_attention_noalloc(const tv_tree_attention_args* args, void* stream);

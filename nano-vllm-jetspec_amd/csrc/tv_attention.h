@@ -37,6 +37,7 @@ struct AttnParams {
     const uint64_t* anc;
     int32_t words;
     int32_t num_requests;
+    int32_t total_queries;   // packed rows of Q and O: every request's rows must lie below it
     int32_t num_kv_heads;
     int32_t block_size;
     float c;  // softmax scale * log2(e)

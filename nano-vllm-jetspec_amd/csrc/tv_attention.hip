@@ -24,7 +24,7 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     const int32_t* gr = p.groups + 8 * static_cast<int64_t>(group);
     const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
     if (r < 0 || r >= p.num_requests || h0 < 0 || n0 < 0 || (hpw != 1 && hpw != 2) || first < 0 || ns < 1 ||
-        first > p.num_slots - ns) {
+        first > p.num_slots - ns || gr[6] != p.qpk) {
         if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
     }
@@ -44,6 +44,10 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     const float2* ml = p.ws_ml + static_cast<int64_t>(first) * kRowsPerItem + wr;
     const float* po = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * kHeadDim + 4 * quad;
     const int tn = p.cnt[r], qbase = p.cu[r];
+    if (qbase < 0 || tn < 0 || tn > p.total_queries - qbase) {   // rows outside the packed batch
+        if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+        return;
+    }
     float m = -INFINITY, l = 0.f;
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < ns; s0 += 8) {
@@ -278,6 +282,7 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     p.anc = a->ancestor_words;
     p.words = a->ancestor_words_per_row;
     p.num_requests = a->num_requests;
+    p.total_queries = a->total_queries;
     p.num_kv_heads = a->num_kv_heads;
     p.qpk = qpk;
     p.block_size = a->block_size;
@@ -325,17 +330,28 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_lock;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_for_current_device(void** out) {
+// The scratch address of the device that `stream` belongs to (the thread's current device
+// for the null stream), resolved once per device with that device current.
+int scratch_for_stream_device(hipStream_t stream, void** out) {
     int device = -1;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return fail(TV_ERR_LAUNCH, "tree_attention_noalloc: hipGetDevice: %s", hipGetErrorString(err));
+    hipError_t err = stream ? hipStreamGetDevice(stream, &device) : hipGetDevice(&device);
+    if (err != hipSuccess) {
+        return fail(TV_ERR_LAUNCH, "tree_attention_noalloc: device of the stream: %s", hipGetErrorString(err));
+    }
     if (device < 0 || device >= kMaxDevices) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention_noalloc: device %d beyond %d", device, kMaxDevices);
     }
     std::lock_guard<std::mutex> guard(g_scratch_lock);
     if (!g_scratch_ptr[device]) {
+        int current = -1;
+        err = hipGetDevice(&current);
+        if (err == hipSuccess && current != device) err = hipSetDevice(device);
         void* ptr = nullptr;
-        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err == hipSuccess) err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (current >= 0 && current != device) {
+            const hipError_t restore = hipSetDevice(current);
+            if (err == hipSuccess) err = restore;
+        }
         if (err != hipSuccess || !ptr) {
             return fail(TV_ERR_LAUNCH, "tree_attention_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(err));
         }
@@ -369,7 +385,7 @@ extern "C" int tv_tree_attention_noalloc(const tv_tree_attention_args* a, void* 
     local.workspace = nullptr;
     local.workspace_bytes = 0;
     if (need > 0) {
-        const int code = scratch_for_current_device(&local.workspace);
+        const int code = scratch_for_stream_device(as_stream(stream), &local.workspace);
         if (code != TV_OK) return code;
         local.workspace_bytes = kScratchBytes;
     }

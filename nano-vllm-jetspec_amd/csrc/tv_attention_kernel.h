@@ -206,7 +206,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const bool wave_active = head_ok && (it.n0 + NW * nsub) < tn;
     // Rows past NW * G (G not dividing 32) are padding: they load no Q and store nothing.
     const bool row_ok = head_ok && c < NW * G && node < tn;
-    const int tree_end = (it.flags & 1) ? min(tn, it.n0 + NPW) : 0;
+    const int tree_end = (it.flags & kItemLastChunk) ? min(tn, it.n0 + NPW) : 0;
     const int ntp = (it.kend - it.kbeg + kTileKeys - 1) / kTileKeys;
     const int nt = ntp + (tree_end + kTileKeys - 1) / kTileKeys;
     const int B = p.block_size;
@@ -217,12 +217,23 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const int nkeys = it.kend - it.kbeg;
     const int npages = slot_mode ? 0 : (nkeys > 0 ? (it.kend - 1) / B - page0 + 1 : 0);
     // The planner keeps every item within the LDS page/slot caches, non-empty, inside its
-    // request's prefix and inside the workspace; an item that is not (a plan made for other
-    // metadata) is reported and skipped rather than read past the request's table row.
-    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk) ||
-        it.h0 < 0 || it.n0 < 0 || it.kbeg < 0 || it.kend < it.kbeg || it.kend > plen || it.slot >= p.num_slots) {
-        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
+    // request's prefix and inside the workspace, and lays its nodes out for this G; an item
+    // that is not (a plan made for other metadata or another head grouping), or whose request
+    // names rows outside the packed batch, is reported and skipped rather than read past the
+    // request's table row or the Q/O rows.
+    if (qbase < 0 || tn > p.total_queries - qbase || nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk) ||
+        it.h0 < 0 || it.n0 < 0 || it.kbeg < 0 || it.kend < it.kbeg || it.kend > plen || it.slot >= p.num_slots ||
+        ((it.flags >> kItemGroupShift) & 0xff) != G) {
+        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST | (it.kend > plen ? TV_STATUS_STALE_PLAN : 0));
         return;
+    }
+    // A plan made before the request grew (host plans read the metadata's host copies): its
+    // last chunk ends before the live prefix length, or its last node block ends before the
+    // live node count.  The planned keys and rows are still computed (every address stays in
+    // bounds); the status word says the rest of the request is missing.
+    if (tid == 0 && (((it.flags & kItemLastChunk) && it.kend != plen) ||
+                     ((it.flags & kItemLastBlock) && it.n0 + NPW < tn))) {
+        set_status(p.status, TV_STATUS_STALE_PLAN);
     }
 
     // Page numbers of the prefix chunk and slots of the tree, validated, into LDS, and

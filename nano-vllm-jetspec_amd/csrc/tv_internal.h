@@ -18,6 +18,14 @@ int check_launch(const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Flags word of an attention work item (both planners write it, the kernel checks it
+// against the live metadata): the last prefix chunk of its (request, head group, node
+// block), which also covers the tree; the last node block of its request; and the query
+// heads per KV head the plan was made for.
+constexpr int kItemLastChunk = 1;
+constexpr int kItemLastBlock = 2;
+constexpr int kItemGroupShift = 8;
+
 inline bool aligned(const void* p, uintptr_t a) {
     return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
 }

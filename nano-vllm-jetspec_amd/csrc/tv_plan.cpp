@@ -245,12 +245,13 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
                     it.n0 = nb * npw;
                     it.kbeg = static_cast<int32_t>(std::min<int64_t>(p, c * chunk));
                     it.kend = static_cast<int32_t>(std::min<int64_t>(p, (c + 1) * chunk));
-                    it.flags = (c == nchunks - 1) ? 1 : 0;
+                    it.flags = ((c == nchunks - 1) ? kItemLastChunk : 0) | ((nb == blocks - 1) ? kItemLastBlock : 0) |
+                               (qpk << kItemGroupShift);
                     it.slot = nchunks > 1 ? first_slot + c : -1;
                     it.hpw = hpw;
                     // Node blocks of one (request, head group, chunk) share their K/V
                     // stream, so they get equal cost and stay adjacent after sorting.
-                    it.cost = cost_weight(hpw) * ((it.kend - it.kbeg) + (it.flags ? t : 0));
+                    it.cost = cost_weight(hpw) * ((it.kend - it.kbeg) + ((it.flags & kItemLastChunk) ? t : 0));
                     it.hg = hg;
                     it.chunk = c;
                     it.nb = nb;
@@ -265,7 +266,7 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
                         gr[3] = hpw;
                         gr[4] = first_slot;
                         gr[5] = nchunks;
-                        gr[6] = 0;
+                        gr[6] = qpk;   // the grouping the slots' rows are laid out for
                         gr[7] = 0;
                     }
                     num_slots += nchunks;

@@ -333,7 +333,7 @@ plan_device_kernel(const PlanArgs a) {
         out[2] = nb * nodes_per_item(hpw, a.qpk);
         out[3] = static_cast<int32_t>(min(static_cast<int64_t>(p), c * chunk));
         out[4] = static_cast<int32_t>(min(static_cast<int64_t>(p), (c + 1) * chunk));
-        out[5] = c == nc - 1 ? 1 : 0;
+        out[5] = (c == nc - 1 ? kItemLastChunk : 0) | (nb == NB - 1 ? kItemLastBlock : 0) | (a.qpk << kItemGroupShift);
         out[6] = nc > 1 ? req_slot_off[r] + (hg * NB + nb) * nc + c : -1;
         out[7] = hpw;
     };
@@ -464,7 +464,7 @@ plan_device_kernel(const PlanArgs a) {
                 gr[3] = hpw;
                 gr[4] = req_slot_off[r] + (hg * NB + nb) * nc;
                 gr[5] = nc;
-                gr[6] = 0;
+                gr[6] = a.qpk;   // the grouping the slots' rows are laid out for
                 gr[7] = 0;
             }
         }

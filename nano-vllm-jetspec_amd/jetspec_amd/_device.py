@@ -3,6 +3,7 @@ from __future__ import annotations
 
 from functools import lru_cache
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -58,3 +59,27 @@ def read_and_clear_status(device: torch.device | str | int = "cuda") -> int:
 @lru_cache(maxsize=None)
 def compute_units(index: int) -> int:
     return int(torch.cuda.get_device_properties(index).multi_processor_count)
+
+
+def upload_fields(fields: dict[str, np.ndarray], device: torch.device, *, pinned: bool) -> dict[str, torch.Tensor]:
+    """All fields in one host-to-device transfer: a byte buffer with each field at an offset
+    aligned to its element size (largest elements first), then typed device views by name."""
+    order = sorted(fields, key=lambda name: -fields[name].itemsize)
+    offsets, cursor = {}, 0
+    for name in order:
+        itemsize = fields[name].itemsize
+        cursor = (cursor + itemsize - 1) // itemsize * itemsize
+        offsets[name] = cursor
+        cursor += fields[name].nbytes
+    host = torch.empty(max(cursor, 8), dtype=torch.uint8, pin_memory=pinned)
+    raw = host.numpy()
+    for name in order:
+        array = fields[name]
+        raw[offsets[name]:offsets[name] + array.nbytes] = array.reshape(-1).view(np.uint8)
+    blob = host.to(device, non_blocking=pinned)
+    views = {}
+    for name in order:
+        array = fields[name]
+        typed = torch.int64 if array.dtype == np.int64 else torch.int32
+        views[name] = blob[offsets[name]:offsets[name] + array.nbytes].view(typed)
+    return views

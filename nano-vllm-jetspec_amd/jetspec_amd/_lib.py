@@ -30,6 +30,7 @@ TV_STATUS_BAD_REQUEST = 4
 TV_STATUS_BAD_POSITION = 8
 TV_STATUS_BAD_DEPTH = 16
 TV_STATUS_BAD_BIAS = 32
+TV_STATUS_STALE_PLAN = 64
 
 # Every extern "C" symbol of include/treeverify.h.
 EXPORTED_SYMBOLS = (

@@ -26,9 +26,13 @@ Two launch modes, chosen per call:
   serving constructor built on the device).  Per (metadata, K/V pool, stream) it
   keeps a filled argument block and, when the plan splits prefixes, one partial-
   result workspace that the 36 per-layer launches of a round reuse in stream order.
-  A steady-state call allocates only its output.  Metadata objects are treated as
-  immutable here, as the reference's frozen dataclass is: an object whose device
-  tensors are rewritten in place must be replayed through a captured graph.
+  A steady-state call allocates only its output, and the first call on a new object
+  queues the plan's upload (pinned, asynchronous) without waiting for the stream.
+  Metadata objects are treated as immutable here, as the reference's frozen dataclass
+  is: an object whose device tensors are rewritten in place must be replayed through a
+  captured graph.  The kernel checks every item against the live prefix lengths and
+  node counts, so a plan that an in-place change outgrew sets TV_STATUS_STALE_PLAN
+  (read_and_clear_status) instead of passing silently.
 * Captured (torch.cuda.is_current_stream_capturing()).  The reference's
   PackedTargetGraph (target_graph.py:55-167) captures the forward once against a
   staged metadata object and replays it after copy_-ing each round's metadata into
@@ -227,9 +231,13 @@ def derived_state(metadata, num_kv_heads: int, *, queries_per_kv: int, chunk_key
     if plan is None:
         plan = make_plan(metadata.prefix_lengths, metadata.node_counts_host, num_kv_heads, metadata.block_size,
                          _device.compute_units(device.index), chunk_keys, queries_per_kv=queries_per_kv)
-        plan["items_dev"] = torch.from_numpy(plan["items"]).to(device, non_blocking=False)
-        plan["groups_dev"] = (torch.from_numpy(plan["groups"]).to(device, non_blocking=False)
-                              if plan["num_groups"] else None)
+        # One pinned staging buffer and an asynchronous copy: the serving loop builds a new
+        # metadata object every round, and a pageable copy here would wait for every kernel
+        # already queued on the stream before the round's first attention could be enqueued.
+        staged = _device.upload_fields({"items": plan["items"], "groups": plan["groups"][:plan["num_groups"]]}, device,
+                         pinned=True)
+        plan["items_dev"] = staged["items"]
+        plan["groups_dev"] = staged["groups"] if plan["num_groups"] else None
         per_meta[plan_key] = plan
     return {"ancestor_words": per_meta["ancestor_words"], "words_per_row": per_meta["words_per_row"], **plan}
 

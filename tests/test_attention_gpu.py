@@ -256,8 +256,10 @@ def test_large_configs_sampled_rows(config):
 
 def test_greedy_acceptance_identical_to_oracle():
     """Project outputs through one seeded vocab head; argmax flips only where the oracle's
-    top-2 margin is within 2 * sup error (jetspec_numeric_oracles.py:171-217), and the
-    accepted paths of every request agree."""
+    top-2 margin is within 2 * sup error (jetspec_numeric_oracles.py:171-217), and every
+    request whose oracle path visits no flipped row accepts the same path, correction and
+    outputs (the walk reads the argmax of path nodes only, so a flip elsewhere in the batch
+    cannot change it)."""
     batch = workloads.config2(DEV, seed=21)
     meta = batch.metadata
     out = packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, 4)
@@ -273,6 +275,7 @@ def test_greedy_acceptance_identical_to_oracle():
     assert witness["large_margin_violations"] == 0
     rng = np.random.default_rng(3)
     greedy_gpu, greedy_ref = got.argmax(-1).tolist(), ref.argmax(-1).tolist()
+    compared = 0
     for r, parents in enumerate(batch.parents):
         sl = meta.request_slice(r)
         tokens = [int(t) for t in rng.integers(0, 512, size=len(parents))]
@@ -283,8 +286,11 @@ def test_greedy_acceptance_identical_to_oracle():
         depths = workloads.depths_of(parents)
         a = oracle.accept_walk(greedy_gpu[sl], tokens, depths, children, 15)
         b = oracle.accept_walk(greedy_ref[sl], tokens, depths, children, 15)
-        if witness["argmax_flips"] == 0:
+        if all(greedy_gpu[sl.start + node] == greedy_ref[sl.start + node] for node in b["path"]):
             assert a == b, f"request {r}"
+            compared += 1
+    print(f"[acceptance] paths compared for {compared} of {len(batch.parents)} requests", flush=True)
+    assert compared >= len(batch.parents) - witness["argmax_flips"]
 
 
 @pytest.mark.parametrize("counts,prefixes", [((63,), (65,)), ((63, 31), (65, 0)), ((63, 31, 47), (65, 0, 257))])

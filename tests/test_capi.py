@@ -183,15 +183,19 @@ def check_plan_covers(prefixes, counts, kv_heads, cus, chunk=0, block=256, group
                 assert ranges[0][0] == 0 and ranges[-1][1] == p
                 for a, b in zip(ranges, ranges[1:]):
                     assert a[1] == b[0]
-                assert [f for _, _, f, _ in ranges] == [0] * (len(ranges) - 1) + [1]
+                # flags: last chunk (bit 0), last node block (bit 1), the plan's group size (bits 8-15)
+                assert [f & 1 for _, _, f, _ in ranges] == [0] * (len(ranges) - 1) + [1]
+                assert all(bool(f & 2) == (n0 + npw >= t) for _, _, f, _ in ranges)
+                assert all((f >> 8) & 0xFF == groups and not f & ~0xFF03 for _, _, f, _ in ranges)
                 if len(ranges) > 1:
                     assert all(s >= 0 for _, _, _, s in ranges)
                 else:
                     assert ranges[0][3] == -1
     assert not covered
     assert plan["num_partial_slots"] == len(slots_seen)
-    for r, h0, n0, hpw, first, ns, _, _ in merges.tolist():
+    for r, h0, n0, hpw, first, ns, qpk, zero in merges.tolist():
         assert set(range(first, first + ns)) <= slots_seen
+        assert qpk == groups and zero == 0
     check_order(items.tolist(), counts)
     return plan
 
@@ -215,7 +219,7 @@ def check_order(items, counts):
     window) and the partial last window stays longest first.
     """
     n = len(items)
-    cost = [(kend - kbeg + (counts[r] if flags else 0)) * COST_WEIGHT[hpw]
+    cost = [(kend - kbeg + (counts[r] if flags & 1 else 0)) * COST_WEIGHT[hpw]
             for r, _, _, kbeg, kend, flags, _, hpw in items]
     stream = [(r, h0, kbeg) for r, h0, _, kbeg, _, _, _, _ in items]
     sizes = {}
@@ -367,7 +371,7 @@ def simulated_makespan(plan, counts, cus=256):
     import heapq
     per_xcd = [[0] * (cus // 8) for _ in range(8)]
     for index, (r, _, _, kbeg, kend, flags, _, hpw) in enumerate(plan["items"].tolist()):
-        tiles = (kend - kbeg + 31) // 32 + ((counts[r] + 31) // 32 if flags else 0)
+        tiles = (kend - kbeg + 31) // 32 + ((counts[r] + 31) // 32 if flags & 1 else 0)
         heap = per_xcd[index % 8]
         heapq.heapreplace(heap, heap[0] + COST_WEIGHT[hpw] / 4 * tiles)
     return max(max(h) for h in per_xcd)

@@ -80,3 +80,52 @@ def test_noalloc_refuses_plans_beyond_its_scratch():
     code = lib.tv_tree_attention_noalloc(ctypes.byref(a), None)
     assert code == _lib.TV_ERR_CAPACITY
     assert b"scratch" in lib.tv_last_error()
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import ctypes, sys
+sys.path[:0] = {paths!r}
+import torch
+from jetspec_amd import _device, _lib, read_and_clear_status, workloads
+from test_zz_no_alloc import argument_block
+lib = _lib.library()
+batch = workloads.config1("cuda")
+expect = torch.empty_like(batch.q)
+probe, state = argument_block(batch, expect, None)
+workspace = torch.empty(state["workspace_bytes"], dtype=torch.uint8, device="cuda")
+a, _ = argument_block(batch, expect, workspace)
+_lib.check(lib.tv_tree_attention(ctypes.byref(a), _device.stream_handle(torch.device("cuda"))), "tree_attention")
+got = torch.full_like(batch.q, float("nan"))
+b, _ = argument_block(batch, got, None)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    code = lib.tv_tree_attention_noalloc(ctypes.byref(b), torch.cuda.current_stream().cuda_stream)
+assert code == 0, lib.tv_last_error()
+for replay in range(3):
+    got.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), expect.view(torch.int16)), f"replay {{replay}} differs"
+assert read_and_clear_status("cuda") == 0
+print("first call under capture: 3 replays equal tv_tree_attention", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The process's first tv_tree_attention_noalloc call happens inside a graph capture (the
+    scratch address is looked up then); every replay equals tv_tree_attention bit for bit.  Run
+    in a fresh process so that no earlier call has resolved the scratch."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    tests = Path(__file__).resolve().parent
+    paths = [str(tests), str(tests.parent), str(tests.parent / "nano-vllm-jetspec_amd")]
+    print("[noalloc] first call under capture (subprocess)", flush=True)
+    result = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE.format(paths=paths)],
+                            capture_output=True, text=True, timeout=110)
+    print(result.stdout[-2000:], result.stderr[-2000:], flush=True)
+    assert result.returncode == 0
+    assert "3 replays equal" in result.stdout
