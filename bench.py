@@ -173,6 +173,17 @@ def copy_probe(torch, gib: int = 2, reps: int = 10) -> dict:
     return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9}
 
 
+def samples(ms: list[float]) -> dict:
+    """Per-launch device times of a GPU leg in the reference benchmark's style
+    (jetspec_tree_kernel_benchmark.py:292-297,421-431): the median, with every sample kept."""
+    return {"median_ms": statistics.median(ms), "mean_ms": statistics.mean(ms), "min_ms": min(ms),
+            "max_ms": max(ms), "samples_ms": [round(x, 5) for x in ms]}
+
+
+def event_times(events) -> list[float]:
+    return [e[0].elapsed_time(e[1]) for e in events]
+
+
 def rope_cache(torch, max_positions: int = 40960, dim: int = 128, base: float = 1e6):
     """Qwen3-8B's cos/sin cache (rope_theta 1e6, 40960 positions) as layers/rotary_embedding.py:28-35 builds it."""
     inv_freq = 1.0 / (base ** (torch.arange(0, dim, 2, dtype=torch.float) / dim))
@@ -208,7 +219,8 @@ def rope_leg(batch, torch, steps: int, warmup: int) -> dict:
         launch()
         e[1].record(stream)
     torch.cuda.synchronize()
-    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    times = event_times(events)
+    ms = statistics.mean(times)
     rows, hq, dim = batch.q.shape
     hkv = batch.new_k.shape[1]
     elem = batch.q.element_size()
@@ -216,7 +228,7 @@ def rope_leg(batch, torch, steps: int, warmup: int) -> dict:
     algo = rows * per_row
     gbs = algo / (ms * 1e-3) / 1e9
     return {"kernel": "rope_scatter_kernel", "rows": rows, "ms": ms, "algorithmic_bytes": algo, "achieved": gbs,
-            "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS}
+            "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS, **samples(times)}
 
 
 def accept_leg(batch, torch, steps: int, warmup: int, vocab: int = 151936) -> dict:
@@ -244,17 +256,20 @@ def accept_leg(batch, torch, steps: int, warmup: int, vocab: int = 151936) -> di
             fn()
             e[1].record(stream)
         torch.cuda.synchronize()
-        return statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+        return event_times(events)
 
-    argmax_ms = timed(lambda: greedy_argmax(logits))
-    torch_ms = timed(lambda: logits.argmax(-1))
-    accept_ms = timed(lambda: accept_batch_device(logits, tokens, parents, depths, cu, 15))
+    argmax_times = timed(lambda: greedy_argmax(logits))
+    torch_times = timed(lambda: logits.argmax(-1))
+    accept_times = timed(lambda: accept_batch_device(logits, tokens, parents, depths, cu, 15))
+    argmax_ms, torch_ms, accept_ms = (statistics.mean(t) for t in (argmax_times, torch_times, accept_times))
     algo = rows * vocab * logits.element_size()
     gbs = algo / (argmax_ms * 1e-3) / 1e9
     del logits
     return {"kernel": "argmax_rows_kernel", "rows": rows, "vocab": vocab, "argmax_ms": argmax_ms,
             "torch_argmax_ms": torch_ms, "argmax_plus_walk_ms": accept_ms, "algorithmic_bytes": algo,
-            "achieved": gbs, "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS}
+            "achieved": gbs, "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": gbs / HBM_PEAK_GBS,
+            **samples(argmax_times), "torch_argmax_median_ms": statistics.median(torch_times),
+            "argmax_plus_walk_median_ms": statistics.median(accept_times)}
 
 
 def graph_leg(batch, torch, steps: int, warmup: int, layers: int = 36) -> dict:
@@ -311,6 +326,135 @@ def graph_leg(batch, torch, steps: int, warmup: int, layers: int = 36) -> dict:
             "speedup": eager_ms / replay_ms, "bitwise_equal": same}
 
 
+def round_leg(batch, torch, rounds: int, layers: int = 36, vocab: int = 151936) -> dict:
+    """One whole verify round of the hot path on the batch's requests: for each of the 36 layers
+    the tree K/V append (store_kvcache into the scratch slots) and the packed attention, then
+    greedy acceptance (device argmax over Qwen3's vocabulary + tree walk), the max_new_tokens /
+    EOS cut, the commit maps and the accepted-only commit of every layer (copy_accepted_kv).
+
+    The reference's round (batch_runtime.py:496-655, state.py:800-926) runs these per layer and
+    then once per round.  Every layer's attention reads the batch's pool: its K/V (GBs) is far
+    larger than the 256 MB Infinity Cache, so each layer streams it from HBM as 36 distinct
+    layers would (36 of config 4's pools would need ~230 GB).  The commit moves rows of a
+    36-layer pool holding the tree scratch pages (the batch's scratch pages renumbered) and two
+    fresh pages per request after its prefix.  Tree tokens are set so that each request accepts
+    the ancestor chain of one seeded node (1 to depth + 1 rows, as config 3 draws them).  As in
+    the reference, the host reads the accepted row count once, before the commit.  Device time
+    (events, the host turnaround excluded) and wall time per round; the median over rounds,
+    every round kept."""
+    import numpy as np
+
+    from jetspec_amd import (accept_batch_device, commit_slots, copy_accepted_kv, packed_tree_attention,
+                             store_kvcache, truncate_accepted, workloads)
+
+    meta = batch.metadata
+    requests, rows, block = meta.num_requests, meta.total_queries, meta.block_size
+    rng = np.random.default_rng(17)
+    logits = torch.randn(rows, vocab, device="cuda", dtype=torch.bfloat16)
+    greedy = logits.argmax(-1).cpu().numpy()
+    tokens = rng.integers(0, vocab, size=rows)
+    parents_flat, depths_flat, chosen = [], [], []
+    for r, parents in enumerate(batch.parents):
+        base = meta.request_slice(r).start
+        depth = workloads.depths_of(parents)
+        # The walk accepts at most max_depth + 1 = 16 nodes (serving_ops.py:78-83).
+        length = int(rng.integers(1, min(max(depth), 15) + 2))
+        candidates = [n for n in range(len(parents)) if depth[n] == length - 1]
+        node = int(candidates[rng.integers(len(candidates))])
+        chain = [node]
+        while parents[chain[-1]] != -1:
+            chain.append(parents[chain[-1]])
+        chain = chain[::-1]
+        on_chain = set(chain)
+        # The chain's children carry their parent's argmax; no other child of a chain node does,
+        # so the walk takes exactly the chain and stops at its end.
+        for n in range(1, len(parents)):
+            want = greedy[base + parents[n]]
+            if n in on_chain:
+                tokens[base + n] = want
+            elif parents[n] in on_chain and tokens[base + n] == want:
+                tokens[base + n] = (want + 1) % vocab
+        parents_flat += list(parents)
+        depths_flat += list(depth)
+        chosen.append(chain)
+    accepted_rows = sum(len(c) for c in chosen)
+    tokens_dev = torch.as_tensor(tokens, dtype=torch.int64, device="cuda")
+    parents_dev = torch.as_tensor(parents_flat, dtype=torch.int64, device="cuda")
+    depths_dev = torch.as_tensor(depths_flat, dtype=torch.int64, device="cuda")
+    budgets = torch.full((requests,), 1 << 20, dtype=torch.int32, device="cuda")
+    ignore_eos = torch.ones(requests, dtype=torch.uint8, device="cuda")
+    # The commit's 36-layer pool: the batch's tree scratch pages, then two pages per request that
+    # hold positions prefix .. prefix + 16 (a request's next positions, state.py:782-785).
+    slot_ids = np.asarray(meta.tree_slot_ids, dtype=np.int64)
+    scratch_pages = sorted(set((slot_ids // block).tolist()))
+    renumber = {page: i for i, page in enumerate(scratch_pages)}
+    commit_tree_slots = torch.as_tensor(
+        np.array([renumber[s // block] * block + s % block for s in slot_ids.tolist()], dtype=np.int64), device="cuda")
+    width = max(p // block for p in meta.prefix_lengths) + 2
+    tables = np.full((requests, width), -1, dtype=np.int32)
+    for r, prefix in enumerate(meta.prefix_lengths):
+        tables[r, prefix // block] = len(scratch_pages) + 2 * r
+        tables[r, prefix // block + 1] = len(scratch_pages) + 2 * r + 1
+    pages = len(scratch_pages) + 2 * requests
+    kv36 = torch.empty((2, layers, pages, block, batch.kv_heads, 128), dtype=batch.k_pool.dtype, device="cuda")
+    kv36.normal_(generator=torch.Generator(device="cuda").manual_seed(36))
+    tables_dev = torch.as_tensor(tables, device="cuda")
+    cache_lens = torch.as_tensor(meta.prefix_lengths, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def one_round(events):
+        events[0].record(stream)
+        for _ in range(layers):
+            store_kvcache(batch.new_k, batch.new_v, batch.k_pool, batch.v_pool, meta.tree_slots)
+            packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, batch.groups)
+        events[1].record(stream)
+        _, paths, lengths, corrections = accept_batch_device(logits, tokens_dev, parents_dev, depths_dev,
+                                                             meta.cu_seqlens_q, 15)
+        _, _, commit_paths, commit_offsets = truncate_accepted(paths, lengths, corrections, tokens_dev,
+                                                               meta.cu_seqlens_q, budgets, ignore_eos, [])
+        source, destination = commit_slots(commit_tree_slots, meta.cu_seqlens_q, commit_paths, commit_offsets,
+                                           tables_dev, cache_lens, block, pages)
+        events[2].record(stream)
+        n = int(commit_offsets[-1].item())   # the one host read of the round
+        events[3].record(stream)
+        payload = copy_accepted_kv(kv36, source[:n], destination[:n], block)
+        events[4].record(stream)
+        return n, payload
+
+    for _ in range(2):
+        one_round([torch.cuda.Event(enable_timing=True) for _ in range(5)])
+    torch.cuda.synchronize()
+    record, walls = [], []
+    for _ in range(rounds):
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        t0 = time.perf_counter()
+        n, payload = one_round(events)
+        torch.cuda.synchronize()
+        walls.append((time.perf_counter() - t0) * 1e3)
+        record.append((events[0].elapsed_time(events[1]), events[1].elapsed_time(events[2]),
+                       events[3].elapsed_time(events[4])))
+    if n != accepted_rows:
+        raise RuntimeError(f"round leg accepted {n} rows, expected {accepted_rows}")
+    layer_ms = [a for a, _, _ in record]
+    accept_ms = [b for _, b, _ in record]
+    commit_ms = [c for _, _, c in record]
+    device_ms = [a + b + c for a, b, c in record]
+    layer_bytes = layers * (batch.algorithmic_bytes() + batch.append_bytes())
+    accept_bytes = rows * vocab * logits.element_size()
+    commit_bytes = 2 * payload   # every payload byte read once and written once
+    total = layer_bytes + accept_bytes + commit_bytes
+    ms = statistics.median(device_ms)
+    del logits, kv36
+    return {"layers": layers, "requests": requests, "tree_rows": rows, "accepted_rows": n,
+            "device_ms_median": ms, "wall_ms_median": statistics.median(walls),
+            "layers_ms_median": statistics.median(layer_ms), "accept_ms_median": statistics.median(accept_ms),
+            "commit_ms_median": statistics.median(commit_ms),
+            "algorithmic_bytes": total, "layers_bytes": layer_bytes, "accept_bytes": accept_bytes,
+            "commit_bytes": commit_bytes, "achieved_gbs": total / (ms * 1e-3) / 1e9,
+            "frac": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "device_samples_ms": [round(x, 4) for x in device_ms], "wall_samples_ms": [round(x, 4) for x in walls]}
+
+
 def exact_leg(batch, torch, steps: int, warmup: int) -> dict:
     """The explicit FP32-probability entry (backend="reference", paged_backend.py:248-256) on the
     same batch: probabilities kept to ~2^-17 relative in the P.V product (two MFMAs per P.V
@@ -331,12 +475,13 @@ def exact_leg(batch, torch, steps: int, warmup: int) -> dict:
         call()
         e[1].record(stream)
     torch.cuda.synchronize()
-    ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    times = event_times(events)
+    ms = statistics.mean(times)
     algo = batch.algorithmic_bytes()
     gbs = algo / (ms * 1e-3) / 1e9
     return {"kernel": "tree_attention_kernel (exact probabilities)", "backend": "reference", "ms": ms,
             "algorithmic_bytes": algo, "achieved": gbs, "unit": "GB/s", "peak": HBM_PEAK_GBS,
-            "frac": gbs / HBM_PEAK_GBS}
+            "frac": gbs / HBM_PEAK_GBS, **samples(times)}
 
 
 def sustain_leg(batch, torch, seconds: float) -> dict:
@@ -404,8 +549,9 @@ def run_verify(args, torch):
     status = read_and_clear_status("cuda")
     if status:
         raise RuntimeError(f"kernel status bits {status}: an index was out of range")
-    attn_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in events)
-    append_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in events)
+    attn_times = [e[1].elapsed_time(e[2]) for e in events]
+    append_times = [e[0].elapsed_time(e[1]) for e in events]
+    attn_ms, append_ms = statistics.mean(attn_times), statistics.mean(append_times)
     algo_bytes = batch.algorithmic_bytes()
     algo_flops = batch.algorithmic_flops()
     achieved = algo_bytes / (attn_ms * 1e-3) / 1e9
@@ -434,7 +580,11 @@ def run_verify(args, torch):
                                  else None),
                      "kernel": "tree_attention_kernel", "kernel_ms": attn_ms, "algorithmic_bytes": algo_bytes,
                      "algorithmic_flops": algo_flops, "achieved_gbs": achieved, "achieved_tflops": tflops,
-                     "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9},
+                     "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9,
+                     "kernel_ms_median": statistics.median(attn_times),
+                     "kernel_samples_ms": [round(x, 5) for x in attn_times],
+                     "append_ms_median": statistics.median(append_times),
+                     "append_samples_ms": [round(x, 5) for x in append_times]},
     }
     if args.kv_heads != 8:
         result["config"]["shard"] = f"tensor-parallel shard: {batch.kv_heads} of 8 KV heads"
@@ -445,6 +595,7 @@ def run_verify(args, torch):
         result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
         result["exact"] = exact_leg(batch, torch, args.steps, args.warmup)
+        result["round"] = round_leg(batch, torch, rounds=3 if args.config == 4 else 5)
     if args.sustain > 0:
         result["sustained"] = sustain_leg(batch, torch, args.sustain)
     probe = copy_probe(torch)

@@ -151,10 +151,86 @@ def build_examples(verbose: bool = False) -> list[Path]:
     return built
 
 
+_RESOURCE_FIELDS = (("TotalSGPRs", "SGPR"), ("VGPRs", "VGPR"), ("AGPRs", "AGPR"), ("SGPRs Spill", "SGPR spill"),
+                    ("VGPRs Spill", "VGPR spill"), ("ScratchSize [bytes/lane]", "scratch B/lane"),
+                    ("LDS Size [bytes/block]", "LDS B/block"), ("Occupancy [waves/SIMD]", "waves/SIMD"))
+
+
+def _demangle(names: list[str]) -> list[str]:
+    """Readable kernel names: the attention instances as <operand type, probability mode, G>,
+    the others through c++filt when it is installed."""
+    import re
+
+    tool = shutil.which("c++filt")
+    plain = names
+    if tool:
+        # Older demanglers do not know the mangling of __bf16 and _Float16: spell them as
+        # vendor-extended types.
+        spelled = [n.replace("DF16b", "u6__bf16").replace("DF16_", "u8_Float16") for n in names]
+        out = subprocess.run([tool], input="\n".join(spelled), capture_output=True, text=True).stdout.splitlines()
+        plain = out if len(out) == len(names) else names
+    readable = []
+    for name, fallback in zip(names, plain):
+        m = re.search(r"tree_attention_kernelI(DF16b|DF16_)Lb([01])ELi(\d+)E", name)
+        if m:
+            operand = "bf16" if m.group(1) == "DF16b" else "f16"
+            mode = "exact P" if m.group(2) == "1" else f"{operand} P"
+            readable.append(f"tree_attention_kernel<{operand}, {mode}, G={m.group(3)}>")
+        else:
+            readable.append(fallback.replace("(anonymous namespace)::", ""))
+    return readable
+
+
+def resource_usage(jobs: int | None = None) -> list[dict]:
+    """The compiler's own resource report (-Rpass-analysis=kernel-resource-usage) for every
+    kernel of every device translation unit: registers, spills, LDS and waves per SIMD."""
+    import re
+    import tempfile
+
+    sources = [s for s in SOURCES if s.endswith(".hip")]
+
+    def report(source: str) -> list[dict]:
+        with tempfile.TemporaryDirectory() as tmp:
+            cmd = [hipcc(), *HIP_FLAGS, f"-I{REPO / 'include'}", f"-I{CSRC}", "-c", "--cuda-device-only",
+                   "-Rpass-analysis=kernel-resource-usage", str(CSRC / source), "-o", str(Path(tmp) / "k.o")]
+            lines = _run(cmd, source + " (resource usage)")
+        kernels, current = [], None
+        for line in lines:
+            m = re.search(r"remark: Function Name: (\S+)", line)
+            if m:
+                current = {"source": source, "kernel": m.group(1)}
+                kernels.append(current)
+                continue
+            m = re.search(r"remark:\s+([^:]+): (\S+) \[-Rpass", line)
+            if m and current is not None:
+                current[m.group(1).strip()] = m.group(2)
+        return kernels
+
+    with ThreadPoolExecutor(jobs or _jobs()) as pool:
+        kernels = [k for ks in pool.map(report, sources) for k in ks]
+    for k, name in zip(kernels, _demangle([k["kernel"] for k in kernels])):
+        k["name"] = name
+    return kernels
+
+
+def resource_table(kernels: list[dict]) -> str:
+    head = "| source | kernel | " + " | ".join(label for _, label in _RESOURCE_FIELDS) + " |"
+    rule = "|---|---|" + "---:|" * len(_RESOURCE_FIELDS)
+    rows = [f"| {k['source']} | `{k['name']}` | " + " | ".join(k.get(field, "") for field, _ in _RESOURCE_FIELDS) + " |"
+            for k in kernels]
+    return "\n".join([head, rule, *rows])
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--verbose", action="store_true")
+    parser.add_argument("--resources", action="store_true",
+                        help="print the compiler's per-kernel resource report (registers, spills, LDS, occupancy) "
+                             "as a markdown table instead of building")
     args = parser.parse_args()
+    if args.resources:
+        print(resource_table(resource_usage()))
+        return 0
     path = build(verbose=args.verbose)
     print(path)
     return 0

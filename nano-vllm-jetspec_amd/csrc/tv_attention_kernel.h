@@ -217,23 +217,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const int nkeys = it.kend - it.kbeg;
     const int npages = slot_mode ? 0 : (nkeys > 0 ? (it.kend - 1) / B - page0 + 1 : 0);
     // The planner keeps every item within the LDS page/slot caches, non-empty, inside its
-    // request's prefix and inside the workspace, and lays its nodes out for this G; an item
-    // that is not (a plan made for other metadata or another head grouping), or whose request
-    // names rows outside the packed batch, is reported and skipped rather than read past the
-    // request's table row or the Q/O rows.
-    if (qbase < 0 || tn > p.total_queries - qbase || nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk) ||
-        it.h0 < 0 || it.n0 < 0 || it.kbeg < 0 || it.kend < it.kbeg || it.kend > plen || it.slot >= p.num_slots ||
-        ((it.flags >> kItemGroupShift) & 0xff) != G) {
-        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST | (it.kend > plen ? TV_STATUS_STALE_PLAN : 0));
+    // request's prefix and inside the workspace; an item that is not (a plan made for other
+    // metadata) is reported and skipped rather than read past the request's table row.
+    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk) ||
+        it.h0 < 0 || it.n0 < 0 || it.kbeg < 0 || it.kend < it.kbeg || it.kend > plen || it.slot >= p.num_slots) {
+        if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
-    }
-    // A plan made before the request grew (host plans read the metadata's host copies): its
-    // last chunk ends before the live prefix length, or its last node block ends before the
-    // live node count.  The planned keys and rows are still computed (every address stays in
-    // bounds); the status word says the rest of the request is missing.
-    if (tid == 0 && (((it.flags & kItemLastChunk) && it.kend != plen) ||
-                     ((it.flags & kItemLastBlock) && it.n0 + NPW < tn))) {
-        set_status(p.status, TV_STATUS_STALE_PLAN);
     }
 
     // Page numbers of the prefix chunk and slots of the tree, validated, into LDS, and
@@ -936,6 +925,27 @@ tree_attention_kernel(const AttnParams p) {
     if (it.r < 0 || it.r >= p.num_requests) {
         if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
+    }
+    // The item against the live metadata.  Refused (reported and skipped): an item laid out
+    // for another query grouping, a request whose rows fall outside the packed batch, and a
+    // chunk past a shrunk prefix (also a stale plan).  Reported only: a plan made before the
+    // request grew (host plans read the metadata's host copies), whose last chunk ends before
+    // the live prefix length or whose last node block ends before the live node count; the
+    // planned keys and rows are still computed, every address in bounds.
+    {
+        const int tn = p.cnt[it.r], qbase = p.cu[it.r], plen = p.plen[it.r];
+        const int npw = (it.hpw == 2 ? 4 : 8) * (32 / G);
+        const bool foreign = ((it.flags >> kItemGroupShift) & 0xff) != G || qbase < 0 || tn > p.total_queries - qbase;
+        const bool shrunk = it.kend > plen;
+        const bool grown = ((it.flags & kItemLastChunk) && it.kend < plen) ||
+                           ((it.flags & kItemLastBlock) && it.n0 + npw < tn);
+        if (foreign || shrunk || grown) {
+            if (threadIdx.x == 0) {
+                set_status(p.status, (foreign || shrunk ? TV_STATUS_BAD_REQUEST : 0) |
+                                     (shrunk || grown ? TV_STATUS_STALE_PLAN : 0));
+            }
+            if (foreign || shrunk) return;
+        }
     }
     switch (it.hpw) {
         case 1: run_item<T, 1, EXACT, G>(p, smem, it); break;
