@@ -64,10 +64,12 @@ store_kvcache_kernel(const char* __restrict__ key, int64_t key_stride_b,
 // overlap takes the staged path:
 //   1. commit_check:   per 256 destinations, OR of {overlap with any source,
 //                      out-of-range slot}; one flag word per workgroup, always
-//                      written, so the workspace needs no clearing.
-//   2. commit_move:    no flag -> every workgroup copies its rows of one (K/V,
-//                      layer) plane directly, all of a thread's loads in flight
-//                      before its stores; overlap alone -> workgroup 0 gathers
+//                      written, so the workspace needs no clearing.  Sources go
+//                      into a hash set in LDS (up to 8192 slots), else tiles of
+//                      them are scanned.
+//   2. commit_move:    no flag -> every workgroup copies its rows of two (K/V,
+//                      layer) planes directly, up to 16 of a thread's loads in
+//                      flight before its stores; overlap alone -> workgroup 0 gathers
 //                      every row into the workspace, synchronises, and scatters
 //                      them (the reference's order; never taken by the served
 //                      callers); an invalid slot -> nothing is written.
@@ -113,6 +115,65 @@ commit_check_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__
     }
 }
 
+// The same flags in O(n) per workgroup for up to kCheckHashMax slots of a pool of fewer than
+// 2^31 slots: every workgroup puts all sources into an open-addressing set in LDS and probes
+// its 256 destinations (the tiled scan above compares each destination with every source,
+// n compares per thread: about 25 us at 4096 slots).
+constexpr int kCheckHash = 16384;                  // set entries (64 KB of LDS), load <= 1/2
+constexpr int64_t kCheckHashMax = kCheckHash / 2;
+
+__device__ __forceinline__ uint32_t check_hash(int32_t v) {
+    return (static_cast<uint32_t>(v) * 2654435761u) >> (32 - 14);   // 14 bits: kCheckHash entries
+}
+static_assert(kCheckHash == 1 << 14, "check_hash takes 14 bits");
+
+__global__ void __launch_bounds__(kCheckThreads)
+commit_check_hash_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t n,
+                         int64_t pool_slots, int32_t* __restrict__ flags, int32_t* status) {
+    __shared__ int32_t table[kCheckHash];
+    __shared__ int32_t block_flag;
+    if (threadIdx.x == 0) block_flag = 0;
+    for (int k = threadIdx.x; k < kCheckHash; k += kCheckThreads) table[k] = -1;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kCheckThreads + threadIdx.x;
+    int32_t flag = 0;
+    int64_t d = -1;
+    if (j < n) {
+        d = dst[j];
+        const int64_t s = src[j];
+        if (d < 0 || d >= pool_slots || s < 0 || s >= pool_slots) flag |= kFlagInvalid;
+    }
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < n; k += kCheckThreads) {
+        const int64_t v = src[k];
+        if (v < 0 || v >= pool_slots) continue;   // reported by its own workgroup
+        uint32_t h = check_hash(static_cast<int32_t>(v));
+        while (true) {
+            const int32_t prev = atomicCAS(&table[h], -1, static_cast<int32_t>(v));
+            if (prev == -1 || prev == static_cast<int32_t>(v)) break;
+            h = (h + 1) & (kCheckHash - 1);
+        }
+    }
+    __syncthreads();
+    if (j < n && !(flag & kFlagInvalid)) {
+        uint32_t h = check_hash(static_cast<int32_t>(d));
+        while (true) {
+            const int32_t e = table[h];
+            if (e == static_cast<int32_t>(d)) {
+                flag |= kFlagOverlap;
+                break;
+            }
+            if (e == -1) break;
+            h = (h + 1) & (kCheckHash - 1);
+        }
+    }
+    if (flag) atomicOr(&block_flag, flag);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        flags[blockIdx.x] = block_flag;
+        if (block_flag & kFlagInvalid) set_status(status, TV_STATUS_BAD_SLOT);
+    }
+}
+
 __device__ __forceinline__ int32_t read_flags(const int32_t* flags, int32_t num_flags) {
     __shared__ int32_t combined;
     if (threadIdx.x == 0) combined = 0;
@@ -137,9 +198,13 @@ __device__ __forceinline__ char* slot_row(const PoolGeom& g, int64_t kv, int64_t
     return g.base + kv * g.s_kv + layer * g.s_layer + block * g.s_block + off * g.s_off;
 }
 
-constexpr int kMoveRows = 8;        // slot rows of one plane per workgroup
+constexpr int kMoveRows = 8;        // slot rows per workgroup
+// (K/V, layer) planes per move workgroup, copied back to back: 2 measured fastest above 512
+// slots (cold caches: 4096 slots 289 -> 244 us, 1848 slots 129 -> 113 us, against 1 plane;
+// 8 and 16 planes 244-248 and 116-120 us).
+constexpr int kMovePlanes = 2;
 constexpr int kMoveThreads = 256;
-constexpr int kMoveUnroll = 8;      // units a thread keeps in flight (16 B each at most)
+constexpr int kMoveUnroll = 16;     // units a thread keeps in flight (16 B each at most)
 
 // Byte offset of `slot`'s row within a (K/V, layer) plane.
 __device__ __forceinline__ int64_t slot_offset(const PoolGeom& g, int64_t slot) {
@@ -148,19 +213,25 @@ __device__ __forceinline__ int64_t slot_offset(const PoolGeom& g, int64_t slot) 
     return block * g.s_block + off * g.s_off;
 }
 
-// Direct copy of up to kMoveRows rows of one (K/V, layer) plane whose byte offsets
-// within the plane are in LDS; rows whose bit is set in `skip` are left alone.  Every
-// thread issues up to kMoveUnroll loads before its stores.
+// Direct copy of up to kMoveRows rows whose byte offsets within a plane are in LDS, in
+// planes plane0 .. plane0 + nplanes - 1; rows whose bit is set in `skip` are left alone.
+// Every thread issues up to kMoveUnroll loads before its stores, and one workgroup's rows
+// of several planes share the slot lookups, so a plane's rows cost no round trip of their
+// own.
+// One plane's rows (the one-launch commit's copiers): the plane base once, 8 loads in flight
+// per thread.  A separate form from copy_rows keeps these small workgroups at 58 VGPRs (8 waves
+// per SIMD); the multi-plane form takes 76 here and measured 2-3 us slower on config 3.
 template <typename Unit>
-__device__ __forceinline__ void copy_rows(const PoolGeom& g, int32_t plane, const int64_t* row_src,
-                                          const int64_t* row_dst, int32_t nrows, uint32_t skip) {
+__device__ __forceinline__ void copy_plane_rows(const PoolGeom& g, int32_t plane, const int64_t* row_src,
+                                                const int64_t* row_dst, int32_t nrows, uint32_t skip) {
+    constexpr int kUnroll = 8;
     char* base = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
     const int32_t upr = g.units_per_row;
     const int32_t total = nrows * upr;
-    for (int32_t u0 = 0; u0 < total; u0 += kMoveThreads * kMoveUnroll) {
-        Unit v[kMoveUnroll];
+    for (int32_t u0 = 0; u0 < total; u0 += kMoveThreads * kUnroll) {
+        Unit v[kUnroll];
 #pragma unroll
-        for (int k = 0; k < kMoveUnroll; ++k) {
+        for (int k = 0; k < kUnroll; ++k) {
             const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
             if (u < total) {
                 const int32_t r = u / upr, c = u - r * upr;
@@ -168,7 +239,7 @@ __device__ __forceinline__ void copy_rows(const PoolGeom& g, int32_t plane, cons
             }
         }
 #pragma unroll
-        for (int k = 0; k < kMoveUnroll; ++k) {
+        for (int k = 0; k < kUnroll; ++k) {
             const int32_t u = u0 + k * kMoveThreads + threadIdx.x;
             if (u < total) {
                 const int32_t r = u / upr, c = u - r * upr;
@@ -178,7 +249,55 @@ __device__ __forceinline__ void copy_rows(const PoolGeom& g, int32_t plane, cons
     }
 }
 
-// Grid (ceil(n / kMoveRows), 2 * layers).  Runs after commit_check on the same stream.
+template <typename Unit, int UNROLL, int MAXP>
+__device__ __forceinline__ void copy_rows(const PoolGeom& g, int32_t plane0, int32_t nplanes, const int64_t* row_src,
+                                          const int64_t* row_dst, int32_t nrows, uint32_t skip) {
+    // Plane bases once per workgroup (a plane is (K/V, layer)); the unit loop divides only
+    // 32-bit unit indices.
+    char* pbase[MAXP];
+#pragma unroll
+    for (int q = 0; q < MAXP; ++q) {
+        const int64_t plane = plane0 + (q < nplanes ? q : nplanes - 1);
+        pbase[q] = g.base + (plane / g.layers) * g.s_kv + (plane % g.layers) * g.s_layer;
+    }
+    const uint32_t upr = static_cast<uint32_t>(g.units_per_row);
+    const uint32_t per_plane = static_cast<uint32_t>(nrows) * upr;
+    const uint32_t total = per_plane * static_cast<uint32_t>(nplanes);
+    auto unit_at = [&](uint32_t u, uint32_t& r, uint32_t& c) -> char* {
+        const uint32_t pl = MAXP == 1 ? 0u : u / per_plane;
+        const uint32_t w = u - pl * per_plane;
+        r = w / upr;
+        c = w - r * upr;
+        char* base = pbase[0];
+#pragma unroll
+        for (int q = 1; q < MAXP; ++q) base = pl == static_cast<uint32_t>(q) ? pbase[q] : base;
+        return base;
+    };
+    for (uint32_t u0 = 0; u0 < total; u0 += kMoveThreads * UNROLL) {
+        Unit v[UNROLL];
+#pragma unroll
+        for (int k = 0; k < UNROLL; ++k) {
+            const uint32_t u = u0 + k * kMoveThreads + threadIdx.x;
+            if (u < total) {
+                uint32_t r, c;
+                const char* base = unit_at(u, r, c);
+                if (!((skip >> r) & 1u)) v[k] = reinterpret_cast<const Unit*>(base + row_src[r])[c];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < UNROLL; ++k) {
+            const uint32_t u = u0 + k * kMoveThreads + threadIdx.x;
+            if (u < total) {
+                uint32_t r, c;
+                char* base = unit_at(u, r, c);
+                if (!((skip >> r) & 1u)) reinterpret_cast<Unit*>(base + row_dst[r])[c] = v[k];
+            }
+        }
+    }
+}
+
+// Grid (ceil(n / kMoveRows), ceil(2 * layers / kMovePlanes)).  Runs after commit_check on
+// the same stream.
 template <typename Unit>
 __global__ void __launch_bounds__(kMoveThreads)
 commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
@@ -214,13 +333,14 @@ commit_move_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* _
         return;
     }
     __shared__ int64_t row_src[kMoveRows], row_dst[kMoveRows];
-    const int32_t plane = blockIdx.y;
+    const int32_t plane0 = blockIdx.y * kMovePlanes;
+    const int32_t nplanes = static_cast<int32_t>(2 * g.layers - plane0 < kMovePlanes ? 2 * g.layers - plane0 : kMovePlanes);
     if (threadIdx.x < nrows) {
         row_src[threadIdx.x] = slot_offset(g, my_src);
         row_dst[threadIdx.x] = slot_offset(g, my_dst);
     }
     __syncthreads();
-    copy_rows<Unit>(g, plane, row_src, row_dst, nrows, 0u);
+    copy_rows<Unit, kMoveUnroll, kMovePlanes>(g, plane0, nplanes, row_src, row_dst, nrows, 0u);
 }
 
 // One-launch commit for up to kFusedMaxSlots slots.  Row i is "dirty" when its
@@ -239,6 +359,8 @@ constexpr int64_t kFusedMaxSlots = 512;
 // against 22.7 us at 8 and 24.3 us at 16 for config 3 with the caches evicted first, and the
 // same 15.8 us warm.
 constexpr int kFusedRows = 4;
+// One (K/V, layer) plane per copier workgroup: 4 and 8 planes per workgroup measured 3.5 and
+// 5.8 us slower on config 3 with the caches evicted (fewer, longer workgroups).
 constexpr int kFusedHash = 2 * kFusedMaxSlots;   // open-addressing slots per hash set (load <= 1/2)
 
 // Open-addressing set of non-negative 32-bit slots in LDS (empty entries are -1),
@@ -357,14 +479,14 @@ commit_fused_kernel(PoolGeom g, const int64_t* __restrict__ src, const int64_t* 
     __syncthreads();
     if (mine) atomicOr(&skip, mine);
     if (__syncthreads_or(bad)) return;
-    copy_rows<Unit>(g, blockIdx.y, row_src, row_dst, nrows, skip);
+    copy_plane_rows<Unit>(g, blockIdx.y, row_src, row_dst, nrows, skip);
 }
 
 template <typename Unit>
 int launch_commit(const PoolGeom& g, const int64_t* src, const int64_t* dst, int32_t* flags,
                   int32_t num_flags, void* staging, hipStream_t stream) {
     const int64_t groups = (g.n + kMoveRows - 1) / kMoveRows;
-    const int64_t planes = 2 * g.layers;
+    const int64_t planes = (2 * g.layers + kMovePlanes - 1) / kMovePlanes;
     if (groups > 0x7fffffff || planes > 65535) {
         return fail(TV_ERR_UNSUPPORTED, "copy_accepted_kv: %lld slots x %lld layers exceed the launch grid",
                     (long long)g.n, (long long)g.layers);
@@ -592,8 +714,13 @@ extern "C" int tv_copy_accepted_kv(void* kv_pool, const int64_t pool_shape[6], c
         if (payload_bytes_host) *payload_bytes_host = payload;
         return TV_OK;
     }
-    hipLaunchKernelGGL(commit_check_kernel, dim3(nflags), dim3(kCheckThreads), 0, s, source_slots,
-                       destination_slots, num_slots, pool_slots, flags, status);
+    if (num_slots <= kCheckHashMax && pool_slots < (int64_t{1} << 31)) {
+        hipLaunchKernelGGL(commit_check_hash_kernel, dim3(nflags), dim3(kCheckThreads), 0, s, source_slots,
+                           destination_slots, num_slots, pool_slots, flags, status);
+    } else {
+        hipLaunchKernelGGL(commit_check_kernel, dim3(nflags), dim3(kCheckThreads), 0, s, source_slots,
+                           destination_slots, num_slots, pool_slots, flags, status);
+    }
     switch (unit) {
         case 16: rc = launch_commit<u32x4>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
         case 8: rc = launch_commit<u32x2>(g, source_slots, destination_slots, flags, nflags, staging, s); break;
