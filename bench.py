@@ -60,6 +60,9 @@ def parse_args():
     parser.add_argument("--groups", type=int, default=4, choices=(1, 2, 3, 4, 5, 6, 7, 8, 16),
                         help="query heads per KV head (4 in the Qwen3-8B geometry; 8 for Qwen3-32B, 16 for "
                              "Qwen3-235B-A22B); other than 4 it is measured on the verify step only")
+    parser.add_argument("--head-dim", type=int, default=128, choices=(64, 128),
+                        help="head size of the batch (128 in the Qwen3 geometry); 64 runs the MFMA kernel's "
+                             "head-size-64 instances, measured on the verify step only")
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
                              "launches); 'all' adds the rope_scatter, accept, graph and exact legs")
@@ -510,6 +513,8 @@ def run_verify(args, torch):
         kwargs["kv_heads"] = args.kv_heads
     if args.groups != 4:
         kwargs["groups"] = args.groups
+    if args.head_dim != 128:
+        kwargs["head_dim"] = args.head_dim
     batch = builder("cuda", **kwargs)
     meta = batch.metadata
     stream = torch.cuda.current_stream()
@@ -569,15 +574,15 @@ def run_verify(args, torch):
                  f"synthetic, diagnostic {args.operands} Q/K/V values (seeded parent arrays, permuted page pool)"),
         "config": {"workload": WORKLOADS[args.config], "requests": meta.num_requests,
                    "tree_rows_per_step": tokens, "prefix_tokens": sum(meta.prefix_lengths),
-                   "q_heads": batch.q_heads, "kv_heads": batch.kv_heads, "head_dim": 128,
+                   "q_heads": batch.q_heads, "kv_heads": batch.kv_heads, "head_dim": batch.head_dim,
                    "page": meta.block_size, "layers_per_step": 1, "pool_pages": batch.info["pages"]},
         "roofline": {"bound": "mfma" if mfma_bound else "hbm",
                      "achieved": tflops if mfma_bound else achieved,
                      "peak": MFMA_BF16_PEAK_TFLOPS if mfma_bound else HBM_PEAK_GBS,
                      "unit": "TFLOP/s" if mfma_bound else "GB/s",
                      "frac": tflops / MFMA_BF16_PEAK_TFLOPS if mfma_bound else achieved / HBM_PEAK_GBS,
-                     "traffic": (traffic_bytes(f"cfg{args.config}") if args.kv_heads == 8 and args.groups == 4
-                                 else None),
+                     "traffic": (traffic_bytes(f"cfg{args.config}")
+                                 if args.kv_heads == 8 and args.groups == 4 and args.head_dim == 128 else None),
                      "kernel": "tree_attention_kernel", "kernel_ms": attn_ms, "algorithmic_bytes": algo_bytes,
                      "algorithmic_flops": algo_flops, "achieved_gbs": achieved, "achieved_tflops": tflops,
                      "append_ms": append_ms, "append_gbs": batch.append_bytes() / (append_ms * 1e-3) / 1e9,
@@ -590,7 +595,7 @@ def run_verify(args, torch):
         result["config"]["shard"] = f"tensor-parallel shard: {batch.kv_heads} of 8 KV heads"
     if args.groups != 4:
         result["config"]["geometry"] = f"{args.groups} query heads per KV head"
-    if args.legs == "all" and args.kv_heads == 8 and args.groups == 4:
+    if args.legs == "all" and args.kv_heads == 8 and args.groups == 4 and args.head_dim == 128:
         result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
         result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
@@ -602,7 +607,7 @@ def run_verify(args, torch):
     result["roofline"]["measured_copy_gbs"] = probe["gbs"]
     result["roofline"]["frac_of_measured_copy"] = achieved / probe["gbs"]
     if (args.cpu_requests > 0 and args.config in (1, 2, 4, 5) and args.operands == "normal"
-            and args.groups == 4 and args.kv_heads == 8):
+            and args.groups == 4 and args.kv_heads == 8 and args.head_dim == 128):
         result["cpu_baseline"] = cpu_baseline(batch, args.cpu_requests)
     return result
 

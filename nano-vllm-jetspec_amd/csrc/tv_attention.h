@@ -49,6 +49,7 @@ struct AttnParams {
     int32_t num_slots;       // partial-result slots the workspace holds (items' and groups' slot bound)
     int32_t* status;
     int32_t qpk;             // query heads per KV head (G; the merge kernel reads it)
+    int32_t head_dim;        // D: 128, or 64 (the d64 instances); partial rows are D floats apart
 };
 
 // Enqueue tree_attention_kernel<operand type, exact probabilities, G> on a grid of
@@ -63,6 +64,13 @@ int launch_tree_attention_g6(const AttnParams& p, int32_t num_items, bool bf16, 
 int launch_tree_attention_g7(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_g8(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_g16(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+// Head size 64 (tv_attention_d64_g<G>.hip), for the power-of-two groups the reference's grouped
+// kernel takes (tree_gqa.py:124-126); other groups at head size 64 run the FP32 kernel.
+int launch_tree_attention_d64_g1(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d64_g2(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d64_g4(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d64_g8(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d64_g16(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 
 namespace {
 

@@ -42,7 +42,10 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     // running maximum rescaled between batches.  Up to 8 partials this is the plain
     // maximum-then-sum.
     const float2* ml = p.ws_ml + static_cast<int64_t>(first) * kRowsPerItem + wr;
-    const float* po = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * kHeadDim + 4 * quad;
+    // Partial rows are D floats apart; quads past D / 4 (head size 64) have nothing to merge.
+    const int D = p.head_dim;
+    if (4 * quad >= D) return;
+    const float* po = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * D + 4 * quad;
     const int tn = p.cnt[r], qbase = p.cu[r];
     if (qbase < 0 || tn < 0 || tn > p.total_queries - qbase) {   // rows outside the packed batch
         if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
@@ -57,7 +60,7 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
         for (int k = 0; k < 8; ++k) {
             if (s0 + k < ns) {
                 part[k] = ml[static_cast<int64_t>(s0 + k) * kRowsPerItem];
-                po4[k] = *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s0 + k) * kRowsPerItem * kHeadDim);
+                po4[k] = *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s0 + k) * kRowsPerItem * D);
             } else {
                 part[k] = make_float2(-INFINITY, 0.f);
                 po4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -174,15 +177,18 @@ namespace {
 // partial-result workspace that `a` names.
 int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     if (!a) return fail(TV_ERR_INVALID, "tree_attention: null args");
-    if (a->head_dim != kHeadDim) {
-        return fail(TV_ERR_UNSUPPORTED, "tree_attention: head_dim %d (implemented: 128)", a->head_dim);
-    }
     const int32_t qpk = a->num_kv_heads >= 1 && a->num_q_heads % a->num_kv_heads == 0
                             ? a->num_q_heads / a->num_kv_heads : 0;
     if (!((qpk >= 1 && qpk <= 8) || qpk == 16)) {
         return fail(TV_ERR_UNSUPPORTED,
                     "tree_attention: %d query heads over %d KV heads (implemented: 1 to 8 or 16 per KV head)",
                     a->num_q_heads, a->num_kv_heads);
+    }
+    const bool pow2_group = (qpk & (qpk - 1)) == 0;
+    if (!(a->head_dim == 128 || (a->head_dim == 64 && pow2_group))) {
+        return fail(TV_ERR_UNSUPPORTED,
+                    "tree_attention: head_dim %d with %d query heads per KV head (implemented: 128, or 64 with "
+                    "1, 2, 4, 8 or 16)", a->head_dim, qpk);
     }
     if (a->prefix_slots ? a->block_size < 1 : (a->block_size < 32 || a->block_size % 32)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: block_size %d is not a multiple of 32", a->block_size);
@@ -285,6 +291,7 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     p.total_queries = a->total_queries;
     p.num_kv_heads = a->num_kv_heads;
     p.qpk = qpk;
+    p.head_dim = a->head_dim;
     p.block_size = a->block_size;
     p.c = a->scale * kLog2e;
     p.items = a->items;
@@ -297,16 +304,26 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     hipStream_t s = as_stream(stream);
     const bool exact = a->exact_probabilities != 0;
     const bool bf16 = a->in_dtype == TV_BF16;
-    switch (qpk) {
-        case 1: launch_tree_attention_g1(p, a->num_items, bf16, exact, s); break;
-        case 2: launch_tree_attention_g2(p, a->num_items, bf16, exact, s); break;
-        case 3: launch_tree_attention_g3(p, a->num_items, bf16, exact, s); break;
-        case 4: launch_tree_attention_g4(p, a->num_items, bf16, exact, s); break;
-        case 5: launch_tree_attention_g5(p, a->num_items, bf16, exact, s); break;
-        case 6: launch_tree_attention_g6(p, a->num_items, bf16, exact, s); break;
-        case 7: launch_tree_attention_g7(p, a->num_items, bf16, exact, s); break;
-        case 8: launch_tree_attention_g8(p, a->num_items, bf16, exact, s); break;
-        default: launch_tree_attention_g16(p, a->num_items, bf16, exact, s); break;
+    if (a->head_dim == 64) {
+        switch (qpk) {
+            case 1: launch_tree_attention_d64_g1(p, a->num_items, bf16, exact, s); break;
+            case 2: launch_tree_attention_d64_g2(p, a->num_items, bf16, exact, s); break;
+            case 4: launch_tree_attention_d64_g4(p, a->num_items, bf16, exact, s); break;
+            case 8: launch_tree_attention_d64_g8(p, a->num_items, bf16, exact, s); break;
+            default: launch_tree_attention_d64_g16(p, a->num_items, bf16, exact, s); break;
+        }
+    } else {
+        switch (qpk) {
+            case 1: launch_tree_attention_g1(p, a->num_items, bf16, exact, s); break;
+            case 2: launch_tree_attention_g2(p, a->num_items, bf16, exact, s); break;
+            case 3: launch_tree_attention_g3(p, a->num_items, bf16, exact, s); break;
+            case 4: launch_tree_attention_g4(p, a->num_items, bf16, exact, s); break;
+            case 5: launch_tree_attention_g5(p, a->num_items, bf16, exact, s); break;
+            case 6: launch_tree_attention_g6(p, a->num_items, bf16, exact, s); break;
+            case 7: launch_tree_attention_g7(p, a->num_items, bf16, exact, s); break;
+            case 8: launch_tree_attention_g8(p, a->num_items, bf16, exact, s); break;
+            default: launch_tree_attention_g16(p, a->num_items, bf16, exact, s); break;
+        }
     }
     if (a->num_groups > 0) {
         const int columns = a->device_counts ? std::min(a->num_groups, kMergeGridCap) : a->num_groups;

@@ -85,12 +85,29 @@ struct Mfma<_Float16> {
     }
 };
 
-// gfx950 LDS serves 256 B per clock from 64 banks.  K operand reads (ds_read_b128,
-// 16 keys at one chunk per clock) need 16 distinct chunk positions; the transposing V
-// reads (4 keys x 4 chunks per clock) need 4 keys spread by multiples of 4 chunks.
-// Both swizzles measured 0 bank conflicts with SQ_LDS_BANK_CONFLICT.
-__device__ __forceinline__ int k_swizzle(int key) { return key & 15; }
-__device__ __forceinline__ int v_swizzle(int key) { return 4 * (key & 3); }
+// Head-dimension geometry, D = 128 (Qwen3) or 64.  A 32-key tile of one head is 32 rows of
+// D elements (2D bytes) in LDS, its 16-byte chunks XOR-swizzled per key.  gfx950 LDS serves
+// 256 B per clock from 64 banks (16 sixteen-byte bank groups):
+//   K operand reads (ds_read_b128): 16 keys at one chunk per clock must land in 16 distinct
+//     bank groups.  D = 128 (256-byte rows, every row starts at group 0): chunk ^ key%16.
+//     D = 64 (128-byte rows, odd rows start at group 8): chunk ^ (key/2)%8 makes the 8 keys
+//     of each row parity take 8 distinct groups.
+//   V^T reads (ds_read_b64_tr_b16, 32 lanes per clock): 4 keys x 4 chunks.  D = 128:
+//     chunk ^ 4*(key%4) spreads the 4 keys over the four 4-group blocks.  D = 64: odd keys
+//     start 8 groups over, so chunk ^ 4*((key/2)%2) separates keys of equal parity.
+// The D = 128 swizzles measured 0 SQ_LDS_BANK_CONFLICT.
+template <int D>
+struct HeadDim {
+    static_assert(D == 64 || D == 128, "head dimension of the MFMA kernel");
+    static constexpr int kSteps = D / 16;          // QK^T MFMAs per tile (16 dims each)
+    static constexpr int kBlocks = D / 32;         // P.V output blocks (32 dims each)
+    static constexpr int kChunks = D / 8;          // 16-byte chunks per row
+    static constexpr int kRow = 2 * D;             // bytes of one K or V row (bf16/f16)
+    static constexpr int kTile = kTileKeys * kRow; // one head's K (or V) tile
+    static constexpr int kSlots = 2 * kSteps;      // MFMA slots of the tile step (QK^T and P.V alternate)
+    static __device__ __forceinline__ int k_swizzle(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
+    static __device__ __forceinline__ int v_swizzle(int key) { return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1); }
+};
 
 
 // s_waitcnt immediate that waits for vmcnt <= n and leaves expcnt/lgkmcnt alone.
@@ -163,8 +180,6 @@ __device__ __forceinline__ void order_point() { __builtin_amdgcn_sched_barrier(0
 // its slot (the tile step has a branchy scalar section in its middle).
 __device__ __forceinline__ void pin(float x) { asm volatile("" : : "v"(x)); }
 
-// MFMA slot of the tile step before which the step's softmax block is issued (of 16).
-constexpr int kSoftmaxSlot = 8;
 // LDS operands are read this many MFMA slots ahead of their use (4 measured 1 % faster than
 // 2 on the long-context batches, 3 no faster than 2).
 constexpr int kReadAhead = 4;
@@ -173,8 +188,9 @@ constexpr int kReadAhead = 4;
 // 2^-17 relative in the P.V product: it is split into a rounded operand-type part and the
 // operand-type rounding of the remainder, and both are multiplied into O (two MFMAs), with
 // the row sums taken in fp32; otherwise the probability is rounded to the operand type once.
-template <typename T, int HPW, bool EXACT, int G>
+template <typename T, int HPW, bool EXACT, int G, int D>
 __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it) {
+    typedef HeadDim<D> HD;
     typedef typename Mfma<T>::vec V8;
     typedef typename Mfma<T>::pair V2;
     typedef __attribute__((address_space(3))) char lds_char;
@@ -185,10 +201,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // LDS ring of NS stages.  K tiles, V tiles and ancestor words live in three regions
     // so every operand address is a per-lane constant plus a compile-time stage offset.
     constexpr int NS = HPW == 1 ? 8 : 4;
-    constexpr int TILE_SET = HPW * kTileBytes;          // K (or V) of the HPW heads, one stage
+    constexpr int TILE_SET = HPW * HD::kTile;           // K (or V) of the HPW heads, one stage
     constexpr int V_REGION = NS * TILE_SET;
     constexpr int M_REGION = 2 * NS * TILE_SET;
-    constexpr int LPT = 2 * HPW;                        // DMA loads per tile per wave, at least
+    // DMA loads per tile per wave, at least: a K and a V load per head at D = 128 (each wave
+    // moves 4 keys, 16 lanes per key); at D = 64 waves 0-3 move K and waves 4-7 V, 8 keys each.
+    constexpr int LPT = D == 128 ? 2 * HPW : HPW;
     static_assert(M_REGION + NS * kMaskBytes <= kRingBytes, "ring exceeds its LDS region");
 
     // `wave` is the same in all lanes; readfirstlane lets the compiler see that, so
@@ -253,12 +271,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         if (tid + k * kThreads < tree_end) sl[k] = p.tree_slots[qbase + tid + k * kThreads];
     }
     // Q^T operand: lane (c, g) holds score row c, dims 16*st + 8*g + 0..7.
-    V8 qb[8];
+    V8 qb[HD::kSteps];
     {
         const T* qrow = static_cast<const T*>(p.q) + static_cast<int64_t>(qbase + node) * p.q_s0 +
                         static_cast<int64_t>(qh) * p.q_s1 + 8 * g;
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
+        for (int st = 0; st < HD::kSteps; ++st) {
             u32x4 raw = {0u, 0u, 0u, 0u};
             if (row_ok) raw = *reinterpret_cast<const u32x4*>(qrow + 16 * st);
             qb[st] = __builtin_bit_cast(V8, raw);
@@ -306,19 +324,19 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // Per-lane LDS operand offsets (stage 0).
     //   K, MFMA step st: key c, chunk 2*st+g at position (2*st+g) ^ (c%16).
     //   V, output block db: key vk (+16*kk+8*h), chunk 4*db+vc at position ^ 4*(vk%4).
-    uint32_t k_ofs[8];
+    uint32_t k_ofs[HD::kSteps];
 #pragma unroll
-    for (int st = 0; st < 8; ++st) {
-        k_ofs[st] = hl * kTileBytes + c * kRowBytes + (((2 * st + g) ^ k_swizzle(c)) & 15) * 16;
+    for (int st = 0; st < HD::kSteps; ++st) {
+        k_ofs[st] = hl * HD::kTile + c * HD::kRow + (((2 * st + g) ^ HD::k_swizzle(c)) & (HD::kChunks - 1)) * 16;
     }
     const int grp = lane >> 4, src = lane & 15;
     const int vk = 4 * (grp >> 1) + (src >> 2);
     const int vc = 2 * (grp & 1) + ((src & 3) >> 1);
-    uint32_t v_ofs[4];
+    uint32_t v_ofs[HD::kBlocks];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-        v_ofs[db] = V_REGION + hl * kTileBytes + vk * kRowBytes + (((4 * db + vc) ^ v_swizzle(vk)) & 15) * 16 +
-                    (src & 1) * 8;
+    for (int db = 0; db < HD::kBlocks; ++db) {
+        v_ofs[db] = V_REGION + hl * HD::kTile + vk * HD::kRow +
+                    (((4 * db + vc) ^ HD::v_swizzle(vk)) & (HD::kChunks - 1)) * 16 + (src & 1) * 8;
     }
     const uint32_t m_ofs = M_REGION + wave * 256 + 4 * (c / G);
 
@@ -328,9 +346,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // that key's row, i.e. global chunk (L%16) ^ swizzle(key).  Every load takes a
     // per-lane 64-bit address: for a prefix tile the tile's page base (scalar
     // arithmetic) plus a per-lane byte offset, for a tree tile the lane's own slot.
-    const int s_key = tid >> 4;
-    const int k_chunk = (lane & 15) ^ k_swizzle(s_key);
-    const int v_chunk = (lane & 15) ^ v_swizzle(s_key);
+    // At D = 128 wave w moves keys 4w..4w+3 of every tile (16 lanes per key); at D = 64 wave w
+    // moves keys 8(w%4)..8(w%4)+7 (8 lanes per key) of K (w < 4) or V (w >= 4).
+    const int s_key = D == 128 ? (tid >> 4) : 8 * (wave & 3) + (lane >> 3);
+    const int k_chunk = (lane & (HD::kChunks - 1)) ^ HD::k_swizzle(s_key);
+    const int v_chunk = (lane & (HD::kChunks - 1)) ^ HD::v_swizzle(s_key);
+    const bool k_wave = D == 128 || wave < 4;   // D = 64: this wave's DMA moves K (else V)
     const uint32_t k_chunk_b = 16u * k_chunk, v_chunk_b = 16u * v_chunk;
     // Byte strides; the host checks that a page stride fits 32 bits and 32 key rows 31.
     const uint32_t k_page_b = static_cast<uint32_t>(p.k_s0 * static_cast<int64_t>(sizeof(T)));
@@ -429,7 +450,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // base opaque at each use, so the compiler emits one scalar add per DMA instead of
     // keeping every stage address live (and spilled).
     const uint32_t lds_base = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-    const uint32_t wave_tile_lds = lds_base + wave * 1024;
+    // Each wave's DMA fills 1 KB of a tile (4 keys at D = 128, 8 at D = 64); at D = 64 the V
+    // waves' part lies in the V region.
+    const uint32_t wave_tile_lds = lds_base + (D == 128 ? wave : (wave & 3)) * 1024 + (k_wave ? 0 : V_REGION);
     const uint32_t wave_mask_lds = lds_base + M_REGION + wave * 256;
     auto tile_dst = [&](int offset) {
         uint32_t base = wave_tile_lds;
@@ -442,25 +465,35 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         return base + static_cast<uint32_t>(offset);
     };
     auto issue_k = [&](int stage, int j) {
-        dma_b128(reinterpret_cast<const void*>(dk + k_hstep_b[j]), tile_dst(stage * TILE_SET + j * kTileBytes));
+        dma_b128(reinterpret_cast<const void*>(dk + k_hstep_b[j]), tile_dst(stage * TILE_SET + j * HD::kTile));
     };
     auto issue_v = [&](int stage, int j) {
         dma_b128(reinterpret_cast<const void*>(dv + v_hstep_b[j]),
-                 tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+                 tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
+    };
+    // D = 64: this wave's one load per head and tile, K or V (wave_tile_lds holds the region).
+    auto issue_kv = [&](int stage, int j) {
+        const uint64_t src = k_wave ? dk + k_hstep_b[j] : dv + v_hstep_b[j];
+        dma_b128(reinterpret_cast<const void*>(src), tile_dst(stage * TILE_SET + j * HD::kTile));
     };
     auto issue_mask = [&](int stage) {
         if (dtree) dma_b32_s(m_lane_b, uniform_ptr(anc_req + dmask), mask_dst(stage * kMaskBytes));
     };
     auto issue_all = [&](int stage) {
+        if constexpr (D == 128) {
 #pragma unroll
-        for (int j = 0; j < HPW; ++j) issue_k(stage, j);
+            for (int j = 0; j < HPW; ++j) issue_k(stage, j);
 #pragma unroll
-        for (int j = 0; j < HPW; ++j) issue_v(stage, j);
+            for (int j = 0; j < HPW; ++j) issue_v(stage, j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) issue_kv(stage, j);
+        }
         issue_mask(stage);
     };
-    f32x16 acc[4];
+    f32x16 acc[HD::kBlocks];
 #pragma unroll
-    for (int db = 0; db < 4; ++db) acc[db] = f32x16{};
+    for (int db = 0; db < HD::kBlocks; ++db) acc[db] = f32x16{};
     // Per row: reference maximum m_run (score units), -m_run*cs, and this lane's half
     // of the running sum.
     float m_run = -INFINITY, nmc = 0.f, l_run = 0.f;
@@ -506,7 +539,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             const float alpha = __builtin_amdgcn_exp2f((m_run - row_max) * cs);
             l_run *= alpha;
 #pragma unroll
-            for (int db = 0; db < 4; ++db) acc[db] *= alpha;
+            for (int db = 0; db < HD::kBlocks; ++db) acc[db] *= alpha;
             m_run = row_max;
             nmc = -row_max * cs;
         }
@@ -541,7 +574,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // between the 8 QK^T steps of tile t+1 and the 8 P.V steps of tile t-1 (whose
     // probabilities were packed in the previous step), every LDS operand is read
     // kReadAhead slots ahead of its use, and the softmax VALU work of tile t (16 exp2, the bf16
-    // packing, the row sums) runs as one block before slot kSoftmaxSlot.  No MFMA of the
+    // packing, the row sums) runs as one block halfway through the step's MFMA slots (before
+    // slot 8 of 16 at D = 128; slots 2, 4, 6, 10, 12 or after 16 measured slower).  No MFMA of the
     // step waits for a VALU result of the same step.  The block, rather than one exp2
     // per slot, keeps each wave's MFMAs back to back while the other wave of its SIMD
     // fills the matrix core; it measured 3-3.5 % faster on the long-context batches.
@@ -549,8 +583,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     auto step = [&](const f32x16& s, f32x16& sn, const V8 (&pb_prev)[2], V8 (&pb)[2], const V8 (&pl_prev)[2],
                     V8 (&pl)[2], const int kst,
                     const int vst, auto&& piece) -> float {
-        V8 ka[8];
-        i16x4 vlo[8], vhi[8];
+        V8 ka[HD::kSteps];
+        i16x4 vlo[HD::kSteps], vhi[HD::kSteps];
         float pr[16];
         float l0 = 0.f, l1 = 0.f;
         auto kread = [&](int i) {
@@ -558,18 +592,18 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         };
         // P.V step j: k half kk = j / 4, output block db = j % 4.
         auto vread = [&](int j) {
-            const int kk = j >> 2, db = j & 3;
+            const int kk = j / HD::kBlocks, db = j % HD::kBlocks;
             vlo[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * kRowBytes));
+                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * HD::kRow));
             vhi[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * kRowBytes));
+                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * HD::kRow));
         };
         auto slot_mfma = [&](int sl) {
             if ((sl & 1) == 0) {
                 const int i = sl >> 1;
                 sn = Mfma<T>::run(ka[i], qb[i], i == 0 ? f32x16{} : sn);
             } else {
-                const int j = sl >> 1, kk = j >> 2, db = j & 3;
+                const int j = sl >> 1, kk = j / HD::kBlocks, db = j % HD::kBlocks;
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(vlo[j], vhi[j], 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
                 if constexpr (EXACT) acc[db] = Mfma<T>::run(a, pl_prev[kk], acc[db]);
@@ -609,8 +643,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         for (int sl = 0; sl < kReadAhead; ++sl) slot_read(sl);
         order_point();
 #pragma unroll
-        for (int sl = 0; sl < 16; ++sl) {
-            if (sl == kSoftmaxSlot) {
+        for (int sl = 0; sl < HD::kSlots; ++sl) {
+            if (sl == HD::kSlots / 2) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) ex(e);
 #pragma unroll
@@ -620,7 +654,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 order_point();
             }
             slot_mfma(sl);
-            if (sl + kReadAhead < 16) slot_read(sl + kReadAhead);
+            if (sl + kReadAhead < HD::kSlots) slot_read(sl + kReadAhead);
             order_point();
             piece(sl);
             order_point();
@@ -642,8 +676,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         // make that stage's V finite.
         typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 #pragma unroll
-        for (int i = 0; i < TILE_SET / (16 * kThreads); ++i) {
-            *(lds_u32x4*)(lds + V_REGION + (NS - 1) * TILE_SET + 16 * (tid + i * kThreads)) = u32x4{0u, 0u, 0u, 0u};
+        for (int i = tid; i < TILE_SET / 16; i += kThreads) {
+            *(lds_u32x4*)(lds + V_REGION + (NS - 1) * TILE_SET + 16 * i) = u32x4{0u, 0u, 0u, 0u};
         }
     }
 #pragma unroll
@@ -665,11 +699,12 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const uint32_t k_tile_b = kTileKeys * k_key_b, v_tile_b = kTileKeys * v_key_b;
     const uint64_t k_head_u = reinterpret_cast<uint64_t>(uniform_ptr(reinterpret_cast<const void*>(k_head_b)));
     const uint64_t v_head_u = reinterpret_cast<uint64_t>(uniform_ptr(reinterpret_cast<const void*>(v_head_b)));
-    uint32_t k_lane_h[HPW], v_lane_h[HPW];
+    uint32_t k_lane_h[HPW], v_lane_h[HPW], kv_lane_h[HPW];
 #pragma unroll
     for (int j = 0; j < HPW; ++j) {
         k_lane_h[j] = k_lane_b + static_cast<uint32_t>(k_hstep_b[j]);
         v_lane_h[j] = v_lane_b + static_cast<uint32_t>(v_hstep_b[j]);
+        kv_lane_h[j] = k_wave ? k_lane_h[j] : v_lane_h[j];
     }
     if (t_fast > 0) {
         const uint32_t tile_pos = static_cast<uint32_t>(it.kbeg + kTileKeys * (NS - 2));
@@ -684,18 +719,27 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     }
     auto fast_issue_k = [&](auto nt, int stage, int j) {
         if constexpr (decltype(nt)::value) {
-            dma_b128_s_nt(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * kTileBytes));
+            dma_b128_s_nt(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * HD::kTile));
         } else {
-            dma_b128_s(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * kTileBytes));
+            dma_b128_s(k_lane_h[j], reinterpret_cast<const void*>(fk), tile_dst(stage * TILE_SET + j * HD::kTile));
         }
     };
     auto fast_issue_v = [&](auto nt, int stage, int j) {
         if constexpr (decltype(nt)::value) {
             dma_b128_s_nt(v_lane_h[j], reinterpret_cast<const void*>(fv),
-                          tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+                          tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
         } else {
             dma_b128_s(v_lane_h[j], reinterpret_cast<const void*>(fv),
-                       tile_dst(V_REGION + stage * TILE_SET + j * kTileBytes));
+                       tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
+        }
+    };
+    // D = 64: this wave's one streamed load per head and tile, K or V.
+    auto fast_issue_kv = [&](auto nt, int stage, int j) {
+        const void* base = reinterpret_cast<const void*>(k_wave ? fk : fv);
+        if constexpr (decltype(nt)::value) {
+            dma_b128_s_nt(kv_lane_h[j], base, tile_dst(stage * TILE_SET + j * HD::kTile));
+        } else {
+            dma_b128_s(kv_lane_h[j], base, tile_dst(stage * TILE_SET + j * HD::kTile));
         }
     };
     auto fast_advance = [&]() {
@@ -720,7 +764,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     pl_prev[1] = V8{};
     if (wave_active) {
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
+        for (int st = 0; st < HD::kSteps; ++st) {
             const V8 a = __builtin_bit_cast(V8, *(const __attribute__((address_space(3))) u32x4*)(lds + k_ofs[st]));
             s = Mfma<T>::run(a, qb[st], s);
         }
@@ -760,14 +804,19 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     __syncthreads();
                     const int ds = (b + NS - 2) % NS;
                     auto piece = [&](int sl) {
-                        if (HPW == 1) {
-                            if (sl == 4) fast_issue_k(nt, ds, 0);
-                            if (sl == 8) fast_issue_v(nt, ds, 0);
+                        if constexpr (D == 128) {
+                            if (HPW == 1) {
+                                if (sl == 4) fast_issue_k(nt, ds, 0);
+                                if (sl == 8) fast_issue_v(nt, ds, 0);
+                            } else {
+                                if (sl == 3 || sl == 5) fast_issue_k(nt, ds, (sl - 3) >> 1);
+                                if (sl == 7 || sl == 9) fast_issue_v(nt, ds, (sl - 7) >> 1);
+                            }
+                            if (sl == 12) fast_advance();
                         } else {
-                            if (sl == 3 || sl == 5) fast_issue_k(nt, ds, (sl - 3) >> 1);
-                            if (sl == 7 || sl == 9) fast_issue_v(nt, ds, (sl - 7) >> 1);
+                            if (sl == 2 || (HPW == 2 && sl == 4)) fast_issue_kv(nt, ds, (sl - 2) >> 1);
+                            if (sl == 6) fast_advance();
                         }
-                        if (sl == 12) fast_advance();
                     };
                     f32x16& s_cur = sc[b & 1];
                     float lt = step(s_cur, sc[(b + 1) & 1], pp[b & 1], pp[(b + 1) & 1], pr_sets[b & 1],
@@ -798,10 +847,15 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     wait_vmcnt<(NS - 4) * LPT>();
                     __syncthreads();
                     const int ds = (b + NS - 2) % NS;
+                    if constexpr (D == 128) {
 #pragma unroll
-                    for (int j = 0; j < HPW; ++j) fast_issue_k(nt, ds, j);
+                        for (int j = 0; j < HPW; ++j) fast_issue_k(nt, ds, j);
 #pragma unroll
-                    for (int j = 0; j < HPW; ++j) fast_issue_v(nt, ds, j);
+                        for (int j = 0; j < HPW; ++j) fast_issue_v(nt, ds, j);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < HPW; ++j) fast_issue_kv(nt, ds, j);
+                    }
                     fast_advance();
                 }
             }
@@ -826,15 +880,21 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             const int ds = (b + NS - 2) % NS;
             auto piece = [&](int sl) {
                 if (sl == 1) describe(t + NS - 2, pf);
-                if (HPW == 1) {
-                    if (sl == 4) issue_k(ds, 0);
-                    if (sl == 8) issue_v(ds, 0);
+                if constexpr (D == 128) {
+                    if (HPW == 1) {
+                        if (sl == 4) issue_k(ds, 0);
+                        if (sl == 8) issue_v(ds, 0);
+                    } else {
+                        if (sl == 3 || sl == 5) issue_k(ds, (sl - 3) >> 1);
+                        if (sl == 7 || sl == 9) issue_v(ds, (sl - 7) >> 1);
+                    }
+                    if (sl == 12) issue_mask(ds);
+                    if (sl == 13) pf = fetch(t + NS - 1);
                 } else {
-                    if (sl == 3 || sl == 5) issue_k(ds, (sl - 3) >> 1);
-                    if (sl == 7 || sl == 9) issue_v(ds, (sl - 7) >> 1);
+                    if (sl == 2 || (HPW == 2 && sl == 4)) issue_kv(ds, (sl - 2) >> 1);
+                    if (sl == 5) issue_mask(ds);
+                    if (sl == 6) pf = fetch(t + NS - 1);
                 }
-                if (sl == 12) issue_mask(ds);
-                if (sl == 13) pf = fetch(t + NS - 1);
             };
             if (wave_active) {
                 if (t >= nfull && t > 0) mask_tile(s, b, t);
@@ -857,7 +917,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 s = sn;
             } else {
 #pragma unroll
-                for (int sl = 0; sl < 16; ++sl) piece(sl);
+                for (int sl = 0; sl < HD::kSlots; ++sl) piece(sl);
             }
         }
     }
@@ -867,11 +927,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db) {
+            for (int db = 0; db < HD::kBlocks; ++db) {
                 const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * kRowBytes));
+                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * HD::kRow));
                 const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * kRowBytes));
+                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * HD::kRow));
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
                 if constexpr (EXACT) acc[db] = Mfma<T>::run(a, pl_prev[kk], acc[db]);
@@ -888,7 +948,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         const float inv = 1.f / l_run;
         const int64_t row = qbase + node;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < HD::kBlocks; ++db) {
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 const f32x4 o = {acc[db][4 * i4] * inv, acc[db][4 * i4 + 1] * inv, acc[db][4 * i4 + 2] * inv,
@@ -897,9 +957,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             }
         }
     } else {
-        float* wo = p.ws_o + (static_cast<int64_t>(it.slot) * kRowsPerItem + wr) * kHeadDim;
+        // Partial rows are D floats apart (the merge reads them with the same stride).
+        float* wo = p.ws_o + (static_cast<int64_t>(it.slot) * kRowsPerItem + wr) * D;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < HD::kBlocks; ++db) {
 #pragma unroll
             for (int i4 = 0; i4 < 4; ++i4) {
                 const f32x4 o = {acc[db][4 * i4], acc[db][4 * i4 + 1], acc[db][4 * i4 + 2], acc[db][4 * i4 + 3]};
@@ -910,7 +971,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     }
 }
 
-template <typename T, bool EXACT, int G>
+template <typename T, bool EXACT, int G, int D>
 __global__ void __launch_bounds__(kThreads)
 tree_attention_kernel(const AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
@@ -948,27 +1009,27 @@ tree_attention_kernel(const AttnParams p) {
         }
     }
     switch (it.hpw) {
-        case 1: run_item<T, 1, EXACT, G>(p, smem, it); break;
-        case 2: run_item<T, 2, EXACT, G>(p, smem, it); break;
+        case 1: run_item<T, 1, EXACT, G, D>(p, smem, it); break;
+        case 2: run_item<T, 2, EXACT, G, D>(p, smem, it); break;
         default:
             if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
             break;
     }
 }
 
-template <int G>
+template <int G, int D = 128>
 int launch_group(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s) {
     if (bf16) {
         if (exact) {
-            hipLaunchKernelGGL((tree_attention_kernel<__bf16, true, G>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<__bf16, true, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
         } else {
-            hipLaunchKernelGGL((tree_attention_kernel<__bf16, false, G>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<__bf16, false, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
         }
     } else {
         if (exact) {
-            hipLaunchKernelGGL((tree_attention_kernel<_Float16, true, G>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<_Float16, true, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
         } else {
-            hipLaunchKernelGGL((tree_attention_kernel<_Float16, false, G>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<_Float16, false, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
         }
     }
     return TV_OK;   // the caller reads the launch status (check_launch)

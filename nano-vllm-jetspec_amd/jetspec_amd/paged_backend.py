@@ -11,9 +11,9 @@ bf16/f16 products, fp32 accumulation and online softmax, in two probability mode
 relative (two MFMAs: its rounding and the rounding of the remainder) and sum it in
 fp32, the reference's "never BF16 probabilities" (paged_backend.py:248-256).
 
-Batches outside the MFMA kernel's geometry (f32 operands, head sizes other than 128,
-query groups other than 1-8 and 16, page sizes that are not multiples of 32, trees
-above 1024 nodes, unaligned pools) run the FP32 kernel (tv_tree_attention_fp32), as the
+Batches outside the MFMA kernel's geometry (f32 operands, head sizes other than 128 and
+64, query groups other than 1-8 and 16 (1, 2, 4, 8 and 16 at head size 64), page sizes
+that are not multiples of 32, trees above 1024 nodes, unaligned pools) run the FP32 kernel (tv_tree_attention_fp32), as the
 reference's dispatcher runs its scalar FP32 kernel outside its fast kernel's geometry
 (paged_backend.py:288-306).  It reads every metadata value from device memory, needs
 no plan, and is capturable as is.
@@ -63,6 +63,15 @@ _BACKENDS = ("auto", "reference", "prefix", "gqa")
 # powers of two up to 16, tree_gqa.py:124-126; 3, 5, 6 and 7 are the GQA ratios of other
 # Qwen-family checkpoints, e.g. 40 query over 8 KV heads).  Other ratios run the FP32 kernel.
 SUPPORTED_GROUPS = (1, 2, 3, 4, 5, 6, 7, 8, 16)
+# Head size 64 runs the MFMA kernel for the power-of-two groups of the reference's grouped kernel.
+SUPPORTED_GROUPS_D64 = (1, 2, 4, 8, 16)
+
+
+def mfma_head(head_size: int, groups: int) -> bool:
+    """Head size and query group the MFMA kernel is built for."""
+    return (head_size == 128 and groups in SUPPORTED_GROUPS) or (head_size == 64 and groups in SUPPORTED_GROUPS_D64)
+
+
 _FP32_ROUTE = "fp32"     # cache entries of batches that run the FP32 kernel
 _derived: dict[int, dict] = {}
 _derived_lock = threading.Lock()
@@ -100,10 +109,10 @@ def _aligned_rows(t: torch.Tensor) -> bool:
 def _mfma_geometry(q, k_pool, v_pool, metadata) -> bool:
     """True when the MFMA kernel (tv_tree_attention) takes this batch; the others run the
     FP32 kernel.  Mirrors the MFMA entry's limits (csrc/tv_attention.hip)."""
-    if q.dtype not in (torch.bfloat16, torch.float16) or q.shape[-1] != 128:
+    if q.dtype not in (torch.bfloat16, torch.float16):
         return False
     kv_heads = int(k_pool.shape[2])
-    if q.shape[1] % kv_heads or q.shape[1] // kv_heads not in SUPPORTED_GROUPS:
+    if q.shape[1] % kv_heads or not mfma_head(int(q.shape[-1]), q.shape[1] // kv_heads):
         return False
     if metadata.block_size % 32 or max(metadata.node_counts_host, default=0) > 1024:
         return False
@@ -488,7 +497,7 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     # The MFMA kernel reads tree visibility as bits, so a bias other than 0 / -inf (which
     # is added to the score) takes the FP32 kernel.
     mask_bias = bool(((bias == 0) | (bias == float("-inf"))).all())
-    geometry = (q.dtype != torch.float32 and head_size == 128 and num_queries_per_kv in SUPPORTED_GROUPS
+    geometry = (q.dtype != torch.float32 and mfma_head(head_size, num_queries_per_kv)
                 and total_q <= 1024 and k_pool.stride(3) == 1 and v_pool.stride(3) == 1
                 and _aligned_rows(k_pool) and _aligned_rows(v_pool)
                 and int(k_pool.shape[0]) * int(block_size) < (1 << 31))

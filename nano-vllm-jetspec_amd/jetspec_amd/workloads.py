@@ -60,8 +60,8 @@ def ancestor_mask(parents: list[int]) -> np.ndarray:
 @dataclass
 class VerifyBatch:
     """One layer's packed verify inputs."""
-    q: torch.Tensor                 # [Q, groups * KV heads, 128]
-    k_pool: torch.Tensor            # [N, 256, 8, 128]
+    q: torch.Tensor                 # [Q, groups * KV heads, head_dim]
+    k_pool: torch.Tensor            # [N, 256, 8, head_dim]
     v_pool: torch.Tensor
     metadata: PackedTreeMetadata
     new_k: torch.Tensor             # tree K/V to append into metadata.tree_slots
@@ -70,6 +70,7 @@ class VerifyBatch:
     prefix_pages: list[list[int]]
     scale: float = HEAD_DIM ** -0.5
     groups: int = Q_HEADS // KV_HEADS
+    head_dim: int = HEAD_DIM
     name: str = ""
     info: dict = field(default_factory=dict)
 
@@ -88,9 +89,9 @@ class VerifyBatch:
     def algorithmic_bytes(self) -> int:
         """K/V of every visible position once per (request, KV head) + Q read + O write."""
         e = self.q.element_size()
-        kv = sum(2 * (p + t) * self.kv_heads * HEAD_DIM * e
+        kv = sum(2 * (p + t) * self.kv_heads * self.head_dim * e
                  for p, t in zip(self.metadata.prefix_lengths, self.metadata.node_counts_host))
-        qo = 2 * self.total_queries * self.q_heads * HEAD_DIM * e
+        qo = 2 * self.total_queries * self.q_heads * self.head_dim * e
         return kv + qo
 
     def algorithmic_flops(self) -> int:
@@ -98,24 +99,24 @@ class VerifyBatch:
         total = 0
         for prefix, parents in zip(self.metadata.prefix_lengths, self.parents):
             visible = sum(prefix + d + 1 for d in depths_of(parents))
-            total += 4 * self.q_heads * HEAD_DIM * visible
+            total += 4 * self.q_heads * self.head_dim * visible
         return total
 
     def append_bytes(self) -> int:
-        return 2 * 2 * self.total_queries * self.kv_heads * HEAD_DIM * self.new_k.element_size()
+        return 2 * 2 * self.total_queries * self.kv_heads * self.head_dim * self.new_k.element_size()
 
 
 def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: torch.device | str,
                        seed: int, dtype: torch.dtype = torch.bfloat16, pool_fill: float = 1.0,
                        poison: bool = True, name: str = "", kv_heads: int = KV_HEADS,
-                       groups: int = Q_HEADS // KV_HEADS) -> VerifyBatch:
+                       groups: int = Q_HEADS // KV_HEADS, head_dim: int = HEAD_DIM) -> VerifyBatch:
     """Pages and slots from a permuted pool; payloads N(0,1); unused rows NaN if `poison`.
 
     `pool_fill` < 1 sizes the pool so live pages fill that fraction (fragmentation).
     Tree K/V are written into their scratch slots (the post-append state) and also
     returned as `new_k`/`new_v` for timing the append.  `kv_heads` < 8 builds one
     tensor-parallel shard: that many KV heads.  `groups` is the number of query heads
-    per KV head (4 in the Qwen3-8B geometry).
+    per KV head (4 in the Qwen3-8B geometry), `head_dim` the head size (128 there).
     """
     device = torch.device(device)
     rng = np.random.default_rng(seed)
@@ -142,7 +143,7 @@ def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: t
         offset += n
     metadata = PackedTreeMetadata.build(prefixes, tables, slots, masks, BLOCK)
     gen = torch.Generator(device=device).manual_seed(seed)
-    shape = (total_pages, BLOCK, kv_heads, HEAD_DIM)
+    shape = (total_pages, BLOCK, kv_heads, head_dim)
     k_pool = torch.empty(shape, dtype=dtype, device=device)
     v_pool = torch.empty(shape, dtype=dtype, device=device)
     k_pool.normal_(generator=gen)
@@ -154,18 +155,19 @@ def build_verify_batch(prefixes: list[int], trees: list[list[int]], *, device: t
             used[np.asarray(table, dtype=np.int64)[pos // BLOCK] * BLOCK + pos % BLOCK] = True
         used[np.asarray(metadata.tree_slot_ids, dtype=np.int64)] = True
         unused = torch.as_tensor(np.flatnonzero(~used), device=device)
-        k_pool.view(-1, kv_heads, HEAD_DIM)[unused] = float("nan")
-        v_pool.view(-1, kv_heads, HEAD_DIM)[unused] = float("nan")
+        k_pool.view(-1, kv_heads, head_dim)[unused] = float("nan")
+        v_pool.view(-1, kv_heads, head_dim)[unused] = float("nan")
     total_q = metadata.total_queries
-    q = torch.randn((total_q, groups * kv_heads, HEAD_DIM), generator=gen, device=device,
+    q = torch.randn((total_q, groups * kv_heads, head_dim), generator=gen, device=device,
                     dtype=torch.float32).to(dtype)
-    new_k = torch.randn((total_q, kv_heads, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
-    new_v = torch.randn((total_q, kv_heads, HEAD_DIM), generator=gen, device=device, dtype=torch.float32).to(dtype)
+    new_k = torch.randn((total_q, kv_heads, head_dim), generator=gen, device=device, dtype=torch.float32).to(dtype)
+    new_v = torch.randn((total_q, kv_heads, head_dim), generator=gen, device=device, dtype=torch.float32).to(dtype)
     tree_slots = metadata.tree_slots
-    k_pool.view(-1, kv_heads, HEAD_DIM)[tree_slots] = new_k
-    v_pool.view(-1, kv_heads, HEAD_DIM)[tree_slots] = new_v
+    k_pool.view(-1, kv_heads, head_dim)[tree_slots] = new_k
+    v_pool.view(-1, kv_heads, head_dim)[tree_slots] = new_v
     return VerifyBatch(q=q, k_pool=k_pool, v_pool=v_pool, metadata=metadata, new_k=new_k, new_v=new_v,
                        parents=[list(p) for p in trees], prefix_pages=tables, name=name, groups=groups,
+                       scale=head_dim ** -0.5, head_dim=head_dim,
                        info={"pages": total_pages, "pool_fill": pool_fill, "seed": seed})
 
 

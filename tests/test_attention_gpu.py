@@ -29,10 +29,10 @@ def heap_parents(n):
 
 
 def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dtype=torch.bfloat16, seed=317,
-                      block=256, groups=4):
+                      block=256, groups=4, head_dim=128):
     """The reference GPU fixture geometry (tests/test_jetspec_packed_attention.py:109-125) with
     shuffled pages, scattered scratch slots and NaN in every unused pool row; `groups`
-    query heads per KV head."""
+    query heads per KV head of `head_dim` elements."""
     rng = np.random.default_rng(seed)
     prefix_pages = [-(-p // block) for p in prefixes]
     scratch_pages = -(-sum(counts) // block) + 1
@@ -52,14 +52,16 @@ def reference_fixture(prefixes=(65, 0, 257), counts=(63, 31, 47), kv_heads=2, dt
     masks = [torch.as_tensor(workloads.ancestor_mask(p), device=DEV) for p in parents]
     meta = PackedTreeMetadata.build(list(prefixes), tables, slots, masks, block)
     gen = torch.Generator(device=DEV).manual_seed(seed)
-    k = torch.full((total, block, kv_heads, 128), float("nan"), device=DEV, dtype=dtype)
+    k = torch.full((total, block, kv_heads, head_dim), float("nan"), device=DEV, dtype=dtype)
     v = torch.full_like(k, float("nan"))
     live = [torch.as_tensor(np.asarray(t, dtype=np.int64)[np.arange(p) // block] * block + np.arange(p) % block,
                             device=DEV) for t, p in zip(tables, prefixes)]
     live = torch.cat(live + slots)
-    k.view(-1, kv_heads, 128)[live] = torch.randn((live.numel(), kv_heads, 128), generator=gen, device=DEV).to(dtype)
-    v.view(-1, kv_heads, 128)[live] = torch.randn((live.numel(), kv_heads, 128), generator=gen, device=DEV).to(dtype)
-    q = torch.randn((meta.total_queries, kv_heads * groups, 128), generator=gen, device=DEV).to(dtype)
+    k.view(-1, kv_heads, head_dim)[live] = torch.randn((live.numel(), kv_heads, head_dim), generator=gen,
+                                                       device=DEV).to(dtype)
+    v.view(-1, kv_heads, head_dim)[live] = torch.randn((live.numel(), kv_heads, head_dim), generator=gen,
+                                                       device=DEV).to(dtype)
+    q = torch.randn((meta.total_queries, kv_heads * groups, head_dim), generator=gen, device=DEV).to(dtype)
     return q, k, v, meta, slots, masks, parents
 
 

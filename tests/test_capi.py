@@ -132,6 +132,16 @@ def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
                 (256 * 256, 256, 1 << 30, 1)):  # next KV head 2 GiB away
         assert lib.tv_tree_attention(ctypes.byref(args(bad)), None) == _lib.TV_ERR_UNSUPPORTED, bad
         assert b"strides out of range" in lib.tv_last_error()
+    # Head sizes: 128 for every group, 64 for the power-of-two groups; others take the FP32 entry.
+    for head, q_heads, accepted in ((64, 8, True), (64, 32, True), (64, 6, False), (96, 8, False),
+                                    (256, 8, False)):
+        a = args((256 * 256, 256, 128, 1))
+        a.head_dim, a.num_q_heads, a.num_requests = head, q_heads, 1
+        code = lib.tv_tree_attention(ctypes.byref(a), None)
+        if accepted:
+            assert code == _lib.TV_OK, lib.tv_last_error()   # no items: accepted and nothing launched
+        else:
+            assert code == _lib.TV_ERR_UNSUPPORTED and b"head_dim" in lib.tv_last_error(), (head, q_heads)
     big = args((256 * 256, 256, 128, 1))
     big.num_blocks, big.num_requests = (1 << 31) // 256, 1
     assert lib.tv_tree_attention(ctypes.byref(big), None) == _lib.TV_ERR_UNSUPPORTED

@@ -103,15 +103,17 @@ def test_f32_operands_through_every_fp32_entry():
         packed_tree_attention(q, k, v, meta, scale, 4, backend="gqa")
 
 
-@pytest.mark.parametrize("head_dim", [64, 96, 256, 512])
-def test_head_sizes(head_dim):
-    q, k, v, meta, *_ = make_case((300, 0, 1025), (17, 40, 64), head_dim=head_dim, seed=head_dim)
+@pytest.mark.parametrize("head_dim,groups", [(64, 3), (96, 4), (256, 4), (512, 4)])
+def test_head_sizes(head_dim, groups):
+    """Head sizes outside the MFMA kernel's (128 for every group, 64 for the power-of-two
+    groups, tests/test_head64_gpu.py)."""
+    q, k, v, meta, *_ = make_case((300, 0, 1025), (17, 40, 64), head_dim=head_dim, groups=groups, seed=head_dim)
     assert not _mfma_geometry(q, k, v, meta)
     scale = head_dim ** -0.5
-    check(packed_tree_attention(q, k, v, meta, scale, 4), q, k, v, meta, f"D{head_dim} auto", scale=scale)
-    check(packed_tree_attention(q, k, v, meta, scale, 4, output_dtype=torch.float32), q, k, v, meta,
+    check(packed_tree_attention(q, k, v, meta, scale, groups), q, k, v, meta, f"D{head_dim} auto", scale=scale)
+    check(packed_tree_attention(q, k, v, meta, scale, groups, output_dtype=torch.float32), q, k, v, meta,
           f"D{head_dim} f32 out", scale=scale)
-    if head_dim in (64, 256):   # the grouped entry takes any head size as the reference's does
+    if head_dim == 256:   # the grouped entry takes any head size as the reference's does
         check(packed_tree_attention(q, k, v, meta, scale, 4, backend="gqa"), q, k, v, meta, f"D{head_dim} gqa",
               scale=scale)
 
@@ -183,14 +185,14 @@ def test_finite_bias_legacy_entry_adds_it_and_packed_path_flags_it():
 
 
 def test_bad_pages_set_status_without_faulting():
-    q, k, v, meta, *_ = make_case((300, 20), (16, 8), head_dim=64, seed=15)
+    q, k, v, meta, *_ = make_case((300, 20), (16, 8), head_dim=96, seed=15)
     bad = replace(meta, block_tables=meta.block_tables.clone())
     bad.block_tables[0, 0] = 10 ** 6
-    out = packed_tree_attention(q, k, v, bad, 64 ** -0.5, 4)
+    out = packed_tree_attention(q, k, v, bad, 96 ** -0.5, 4)
     torch.cuda.synchronize()
     assert read_and_clear_status(DEV) & _lib.TV_STATUS_BAD_PAGE
     rows = bad.request_slice(1)
-    good = packed_tree_attention(q, k, v, meta, 64 ** -0.5, 4)
+    good = packed_tree_attention(q, k, v, meta, 96 ** -0.5, 4)
     assert torch.equal(out[rows].view(torch.int16), good[rows].view(torch.int16))   # other requests untouched
     assert read_and_clear_status(DEV) == 0
 
@@ -204,9 +206,9 @@ def test_captured_fp32_route_follows_staged_metadata():
     capture against a staged metadata object, then replay after copy_-ing rounds with
     other prefixes and trees of the same signature (target_graph.py:55-75,150-167)."""
     rounds = [((12, 60, 72), (300, 70, 500)), ((24, 36, 84), (510, 25, 257)), ((72, 12, 60), (1, 800, 96))]
-    cases = [make_case(p, c, head_dim=64, seed=40 + i) for i, (c, p) in enumerate(rounds)]
+    cases = [make_case(p, c, head_dim=96, seed=40 + i) for i, (c, p) in enumerate(rounds)]
     pages = max(int(c[1].shape[0]) for c in cases)
-    k = torch.randn((pages, 256, 2, 64), device=DEV).to(torch.bfloat16)
+    k = torch.randn((pages, 256, 2, 96), device=DEV).to(torch.bfloat16)
     v = torch.randn_like(k)
     width = 4
     staged = None
@@ -237,5 +239,5 @@ def test_captured_fp32_route_follows_staged_metadata():
         torch.cuda.synchronize()
         eager = packed_tree_attention(q, k, v, meta, 0.125, 4)
         assert torch.equal(captured.view(torch.int16), eager.view(torch.int16)), f"round {index}"
-        check(captured.clone(), q, k, v, meta, f"captured D64 round {index}", scale=0.125)
+        check(captured.clone(), q, k, v, meta, f"captured D96 round {index}", scale=0.125)
         torch.randn(1 << 20, device=DEV).sum().item()   # eager work between replays
