@@ -60,9 +60,9 @@ def parse_args():
     parser.add_argument("--groups", type=int, default=4, choices=(1, 2, 3, 4, 5, 6, 7, 8, 16),
                         help="query heads per KV head (4 in the Qwen3-8B geometry; 8 for Qwen3-32B, 16 for "
                              "Qwen3-235B-A22B); other than 4 it is measured on the verify step only")
-    parser.add_argument("--head-dim", type=int, default=128, choices=(64, 128),
-                        help="head size of the batch (128 in the Qwen3 geometry); 64 runs the MFMA kernel's "
-                             "head-size-64 instances, measured on the verify step only")
+    parser.add_argument("--head-dim", type=int, default=128, choices=(64, 128, 256),
+                        help="head size of the batch (128 in the Qwen3 geometry); 64 and 256 run the MFMA "
+                             "kernel's instances for those sizes, measured on the verify step only")
     parser.add_argument("--legs", choices=("all", "verify"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
                              "launches); 'all' adds the rope_scatter, accept, graph and exact legs")

@@ -283,7 +283,7 @@ typedef struct tv_attention_plan_info {
     int32_t num_groups;
     int32_t num_partial_slots;
     int32_t ancestor_words_per_row;  /* ceil(max node count / 64) */
-    int64_t workspace_bytes;         /* device workspace tv_tree_attention needs */
+    int64_t workspace_bytes;         /* device workspace tv_tree_attention needs (head_dim <= 128) */
 } tv_attention_plan_info;
 
 int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
@@ -464,13 +464,23 @@ typedef struct tv_tree_attention_args {
  * whose ancestor bit is set (addressed through tree_slots).  bf16/f16 operands,
  * fp32 accumulation and online softmax, probabilities rounded to the operand
  * type for the P.V product (tree_gqa.py:102-105).
- * Implemented geometry: head_dim 128, num_q_heads == G * num_kv_heads with G in
- * 1..8 or 16 (the reference's grouped kernel takes powers of two up to 16,
- * tree_gqa.py:124-126; its FP32 kernel any G, as tv_tree_attention_fp32 does),
+ * Implemented geometry: num_q_heads == G * num_kv_heads with head_dim 128 and G in
+ * 1..8 or 16, or head_dim 64 or 256 and G in 1, 2, 4, 8, 16 (the reference's grouped
+ * kernel takes powers of two up to 16 and pads the head size to a power of two,
+ * tree_gqa.py:124-135; its FP32 kernel any geometry, as tv_tree_attention_fp32 does),
  * block_size % 32 == 0 (any positive block_size with prefix_slots).  The plan must
- * have been made for the same G.
+ * have been made for the same G; plans do not depend on head_dim.  workspace_bytes must
+ * be at least tv_tree_attention_workspace_bytes(num_partial_slots, head_dim).
  */
 int tv_tree_attention(const tv_tree_attention_args* args, void* stream);
+
+/*
+ * Split-prefix workspace tv_tree_attention needs for a plan with num_partial_slots partial
+ * slots at head size head_dim: the plan's workspace_bytes for head sizes up to 128, twice
+ * its partial-row area at 256.  No counterpart in the reference (its kernels keep no
+ * partial results).
+ */
+int64_t tv_tree_attention_workspace_bytes(int32_t num_partial_slots, int32_t head_dim);
 
 /*
  * FP32 tree attention for every geometry the reference accepts: the MI355X form of
@@ -535,7 +545,8 @@ int64_t tv_sizeof_tree_attention_fp32_args(void);
  * loops, harnesses that forbid allocation).  Same arguments, except that `workspace` and
  * `workspace_bytes` are ignored: split prefixes keep their partial results in a scratch
  * array built into the library, one per device, of tv_tree_attention_noalloc_max_workspace()
- * bytes (64 MiB: 500 partial slots, about two rounds of work items on 256 CUs), held until
+ * bytes (64 MiB: 504 partial slots up to head size 128, 254 at 256; about two rounds of work
+ * items on 256 CUs), held until
  * the process ends.  A plan whose partial slots need more returns TV_ERR_CAPACITY and
  * launches nothing.  Every call on one device shares that device's scratch, so calls that
  * overlap on one device (concurrent streams) race; calls ordered on one stream do not.

@@ -25,10 +25,12 @@ ARCH = "gfx950"
 
 # Query heads per KV head the attention kernel is instantiated for.
 GROUPS = (1, 2, 3, 4, 5, 6, 7, 8, 16)
-# ... and at head size 64 for the power-of-two groups.
+# ... and at head sizes 64 and 256 for the power-of-two groups.
 GROUPS_D64 = (1, 2, 4, 8, 16)
+GROUPS_D256 = (1, 2, 4, 8, 16)
 ATTENTION_GROUP_SOURCES = (tuple(f"tv_attention_g{g}.hip" for g in GROUPS) +
-                           tuple(f"tv_attention_d64_g{g}.hip" for g in GROUPS_D64))
+                           tuple(f"tv_attention_d64_g{g}.hip" for g in GROUPS_D64) +
+                           tuple(f"tv_attention_d256_g{g}.hip" for g in GROUPS_D256))
 SOURCES = ("tv_common.cpp", "tv_plan.cpp", "tv_kvcache.hip", "tv_attention.hip", *ATTENTION_GROUP_SOURCES,
            "tv_attention_fp32.hip",
            "tv_rope.hip", "tv_accept.hip", "tv_metadata.hip", "tv_plan_device.hip")

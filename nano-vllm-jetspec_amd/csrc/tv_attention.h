@@ -49,7 +49,8 @@ struct AttnParams {
     int32_t num_slots;       // partial-result slots the workspace holds (items' and groups' slot bound)
     int32_t* status;
     int32_t qpk;             // query heads per KV head (G; the merge kernel reads it)
-    int32_t head_dim;        // D: 128, or 64 (the d64 instances); partial rows are D floats apart
+    int32_t head_dim;        // D: 128, 64 or 256 (the d64/d256 instances); partial rows are D floats apart
+    int32_t num_items;       // items of a host plan (the D = 256 grid covers whole windows of 8)
 };
 
 // Enqueue tree_attention_kernel<operand type, exact probabilities, G> on a grid of
@@ -71,6 +72,12 @@ int launch_tree_attention_d64_g2(const AttnParams& p, int32_t num_items, bool bf
 int launch_tree_attention_d64_g4(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_d64_g8(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 int launch_tree_attention_d64_g16(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+// Head size 256 (tv_attention_d256_g<G>.hip), the same groups; two 4-wave workgroups per item.
+int launch_tree_attention_d256_g1(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d256_g2(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d256_g4(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d256_g8(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
+int launch_tree_attention_d256_g16(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s);
 
 namespace {
 

@@ -42,52 +42,54 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     // running maximum rescaled between batches.  Up to 8 partials this is the plain
     // maximum-then-sum.
     const float2* ml = p.ws_ml + static_cast<int64_t>(first) * kRowsPerItem + wr;
-    // Partial rows are D floats apart; quads past D / 4 (head size 64) have nothing to merge.
+    // Partial rows are D floats apart.  A thread merges dims 4*quad..4*quad+3 and, at head
+    // size 256, the same 128 dims further; quads past D / 4 (head size 64) have none.
     const int D = p.head_dim;
-    if (4 * quad >= D) return;
-    const float* po = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * D + 4 * quad;
+    const float* prow = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * D;
     const int tn = p.cnt[r], qbase = p.cu[r];
     if (qbase < 0 || tn < 0 || tn > p.total_queries - qbase) {   // rows outside the packed batch
         if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
     }
-    float m = -INFINITY, l = 0.f;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-        float2 part[8];
-        f32x4 po4[8];
+    const bool row_ok = head < p.num_kv_heads && node < tn && c < nw * G;   // c >= nw * G: padding row
+    for (int d4 = 4 * quad; d4 < D; d4 += 128) {
+        const float* po = prow + d4;
+        float m = -INFINITY, l = 0.f;
+        f32x4 o = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < ns; s0 += 8) {
+            float2 part[8];
+            f32x4 po4[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (s0 + k < ns) {
-                part[k] = ml[static_cast<int64_t>(s0 + k) * kRowsPerItem];
-                po4[k] = *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s0 + k) * kRowsPerItem * D);
-            } else {
-                part[k] = make_float2(-INFINITY, 0.f);
-                po4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < 8; ++k) {
+                if (s0 + k < ns) {
+                    part[k] = ml[static_cast<int64_t>(s0 + k) * kRowsPerItem];
+                    po4[k] = *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s0 + k) * kRowsPerItem * D);
+                } else {
+                    part[k] = make_float2(-INFINITY, 0.f);
+                    po4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
             }
-        }
-        float mb = m;
+            float mb = m;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) mb = fmaxf(mb, part[k].x);
-        const float mc = (mb == -INFINITY ? 0.f : mb) * p.c;
-        if (m != -INFINITY) {
-            const float keep = __builtin_amdgcn_exp2f(m * p.c - mc);
-            l *= keep;
-            o *= keep;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (s0 + k < ns) {
-                const float w = __builtin_amdgcn_exp2f(part[k].x * p.c - mc);
-                l += part[k].y * w;
-                o += po4[k] * w;
+            for (int k = 0; k < 8; ++k) mb = fmaxf(mb, part[k].x);
+            const float mc = (mb == -INFINITY ? 0.f : mb) * p.c;
+            if (m != -INFINITY) {
+                const float keep = __builtin_amdgcn_exp2f(m * p.c - mc);
+                l *= keep;
+                o *= keep;
             }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (s0 + k < ns) {
+                    const float w = __builtin_amdgcn_exp2f(part[k].x * p.c - mc);
+                    l += part[k].y * w;
+                    o += po4[k] * w;
+                }
+            }
+            m = mb;
         }
-        m = mb;
+        if (row_ok) store_out4<T>(p, qbase + node, qh, d4, o * (1.f / l));
     }
-    if (head >= p.num_kv_heads || node >= tn || c >= nw * G) return;   // c >= nw * G: padding row
-    const float inv = 1.f / l;
-    store_out4<T>(p, qbase + node, qh, 4 * quad, o * inv);
 }
 
 // Grid (groups, 32) for a host plan.  A device-built plan (graph capture) launches at most
@@ -173,6 +175,17 @@ static __device__ __align__(256) char scratch[kScratchBytes];
 
 namespace {
 
+// Split-K workspace of `slots` partial slots: partial O (256 rows of max(D, 128) floats per
+// slot, so head sizes up to 128 share one size), then (max, sum) per row.
+int64_t partial_o_span(int64_t slots, int32_t head_dim) {
+    const int64_t row = head_dim > kHeadDim ? head_dim : kHeadDim;
+    return slots > 0 ? (slots * kRowsPerItem * row * 4 + 255) / 256 * 256 : 0;
+}
+int64_t workspace_need(int64_t slots, int32_t head_dim) {
+    if (slots <= 0) return 0;
+    return partial_o_span(slots, head_dim) + (slots * kRowsPerItem * 8 + 255) / 256 * 256;
+}
+
 // Validates `a` and enqueues the attention (and the merge of split prefixes) with the
 // partial-result workspace that `a` names.
 int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
@@ -185,10 +198,10 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
                     a->num_q_heads, a->num_kv_heads);
     }
     const bool pow2_group = (qpk & (qpk - 1)) == 0;
-    if (!(a->head_dim == 128 || (a->head_dim == 64 && pow2_group))) {
+    if (!(a->head_dim == 128 || ((a->head_dim == 64 || a->head_dim == 256) && pow2_group))) {
         return fail(TV_ERR_UNSUPPORTED,
-                    "tree_attention: head_dim %d with %d query heads per KV head (implemented: 128, or 64 with "
-                    "1, 2, 4, 8 or 16)", a->head_dim, qpk);
+                    "tree_attention: head_dim %d with %d query heads per KV head (implemented: 128, or 64 and 256 "
+                    "with 1, 2, 4, 8 or 16)", a->head_dim, qpk);
     }
     if (a->prefix_slots ? a->block_size < 1 : (a->block_size < 32 || a->block_size % 32)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: block_size %d is not a multiple of 32", a->block_size);
@@ -249,9 +262,8 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
         !a->block_tables || !a->tree_slots || !a->ancestor_words || !a->items) {
         return fail(TV_ERR_INVALID, "tree_attention: null pointer");
     }
-    const int64_t o_bytes = static_cast<int64_t>(a->num_partial_slots) * kRowsPerItem * kHeadDim * 4;
-    const int64_t o_span = (o_bytes + 255) / 256 * 256;
-    const int64_t need = a->num_partial_slots ? o_span + (static_cast<int64_t>(a->num_partial_slots) * kRowsPerItem * 8 + 255) / 256 * 256 : 0;
+    const int64_t o_span = partial_o_span(a->num_partial_slots, a->head_dim);
+    const int64_t need = workspace_need(a->num_partial_slots, a->head_dim);
     if ((a->num_groups > 0 && !a->groups) || (a->num_partial_slots > 0 && !a->workspace)) {
         return fail(TV_ERR_INVALID, "tree_attention: split plan without groups/workspace");
     }
@@ -292,6 +304,7 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     p.num_kv_heads = a->num_kv_heads;
     p.qpk = qpk;
     p.head_dim = a->head_dim;
+    p.num_items = a->num_items;
     p.block_size = a->block_size;
     p.c = a->scale * kLog2e;
     p.items = a->items;
@@ -304,7 +317,15 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     hipStream_t s = as_stream(stream);
     const bool exact = a->exact_probabilities != 0;
     const bool bf16 = a->in_dtype == TV_BF16;
-    if (a->head_dim == 64) {
+    if (a->head_dim == 256) {
+        switch (qpk) {
+            case 1: launch_tree_attention_d256_g1(p, a->num_items, bf16, exact, s); break;
+            case 2: launch_tree_attention_d256_g2(p, a->num_items, bf16, exact, s); break;
+            case 4: launch_tree_attention_d256_g4(p, a->num_items, bf16, exact, s); break;
+            case 8: launch_tree_attention_d256_g8(p, a->num_items, bf16, exact, s); break;
+            default: launch_tree_attention_d256_g16(p, a->num_items, bf16, exact, s); break;
+        }
+    } else if (a->head_dim == 64) {
         switch (qpk) {
             case 1: launch_tree_attention_d64_g1(p, a->num_items, bf16, exact, s); break;
             case 2: launch_tree_attention_d64_g2(p, a->num_items, bf16, exact, s); break;
@@ -336,12 +357,6 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
     return check_launch("tree_attention");
 }
 
-// Split-K workspace bytes a plan with `slots` partial slots needs (partial O, then (max, sum)).
-int64_t workspace_need(int64_t slots) {
-    if (slots <= 0) return 0;
-    const int64_t o_span = (slots * kRowsPerItem * kHeadDim * 4 + 255) / 256 * 256;
-    return o_span + (slots * kRowsPerItem * 8 + 255) / 256 * 256;
-}
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_lock;
@@ -387,11 +402,15 @@ extern "C" int tv_tree_attention(const tv_tree_attention_args* a, void* stream) 
 
 extern "C" int64_t tv_tree_attention_noalloc_max_workspace(void) { return kScratchBytes; }
 
+extern "C" int64_t tv_tree_attention_workspace_bytes(int32_t num_partial_slots, int32_t head_dim) {
+    return workspace_need(num_partial_slots, head_dim);
+}
+
 extern "C" int tv_tree_attention_noalloc(const tv_tree_attention_args* a, void* stream) {
     clear_error();
     if (!a) return fail(TV_ERR_INVALID, "tree_attention_noalloc: null args");
     if (a->num_partial_slots < 0) return fail(TV_ERR_INVALID, "tree_attention_noalloc: invalid counts");
-    const int64_t need = workspace_need(a->num_partial_slots);
+    const int64_t need = workspace_need(a->num_partial_slots, a->head_dim);
     if (need > kScratchBytes) {
         return fail(TV_ERR_CAPACITY,
                     "tree_attention_noalloc: the plan's %d partial slots need %lld workspace bytes, above the "

@@ -52,6 +52,8 @@
 // last 32 - NW * G rows are padding (zero Q, never stored).
 #pragma once
 
+#include <utility>
+
 #include "tv_attention.h"
 
 namespace tv {
@@ -85,26 +87,38 @@ struct Mfma<_Float16> {
     }
 };
 
-// Head-dimension geometry, D = 128 (Qwen3) or 64.  A 32-key tile of one head is 32 rows of
-// D elements (2D bytes) in LDS, its 16-byte chunks XOR-swizzled per key.  gfx950 LDS serves
-// 256 B per clock from 64 banks (16 sixteen-byte bank groups):
+// Head-dimension geometry, D = 128 (Qwen3), 64 or 256.  A 32-key tile of one head is held in
+// LDS as kParts parts of 32 rows x kPartRow bytes: D = 128 one part of 256-byte rows, D = 64
+// one part of 128-byte rows, D = 256 four parts of 128-byte rows (dims 64p..64p+63 in part
+// p), each 16-byte chunk XOR-swizzled per key within its row.  gfx950 LDS serves 256 B per
+// clock from 64 banks (16 sixteen-byte bank groups):
 //   K operand reads (ds_read_b128): 16 keys at one chunk per clock must land in 16 distinct
-//     bank groups.  D = 128 (256-byte rows, every row starts at group 0): chunk ^ key%16.
-//     D = 64 (128-byte rows, odd rows start at group 8): chunk ^ (key/2)%8 makes the 8 keys
-//     of each row parity take 8 distinct groups.
-//   V^T reads (ds_read_b64_tr_b16, 32 lanes per clock): 4 keys x 4 chunks.  D = 128:
-//     chunk ^ 4*(key%4) spreads the 4 keys over the four 4-group blocks.  D = 64: odd keys
-//     start 8 groups over, so chunk ^ 4*((key/2)%2) separates keys of equal parity.
-// The D = 128 swizzles measured 0 SQ_LDS_BANK_CONFLICT.
+//     bank groups.  256-byte rows (every row starts at group 0): chunk ^ key%16.  128-byte
+//     rows (odd rows start at group 8): chunk ^ (key/2)%8 makes the 8 keys of each row
+//     parity take 8 distinct groups.
+//   V^T reads (ds_read_b64_tr_b16, 32 lanes per clock): 4 keys x 4 chunks.  256-byte rows:
+//     chunk ^ 4*(key%4) spreads the 4 keys over the four 4-group blocks.  128-byte rows: odd
+//     keys start 8 groups over, so chunk ^ 4*((key/2)%2) separates keys of equal parity.
+// Both measured 0 SQ_LDS_BANK_CONFLICT.  The 128-byte parts let one DMA lane keep one key for
+// all of a tile's loads at D = 256 (8 lanes per key, one load per part).
+// D = 256 doubles a wave's Q operands and O accumulators (64 + 128 registers per lane), which
+// two waves per SIMD cannot hold: its workgroups have 4 waves (one per SIMD, up to 512
+// registers) and a work item's 256 score rows take two of them (kHalves).
 template <int D>
 struct HeadDim {
-    static_assert(D == 64 || D == 128, "head dimension of the MFMA kernel");
+    static_assert(D == 64 || D == 128 || D == 256, "head dimension of the MFMA kernel");
     static constexpr int kSteps = D / 16;          // QK^T MFMAs per tile (16 dims each)
     static constexpr int kBlocks = D / 32;         // P.V output blocks (32 dims each)
-    static constexpr int kChunks = D / 8;          // 16-byte chunks per row
     static constexpr int kRow = 2 * D;             // bytes of one K or V row (bf16/f16)
     static constexpr int kTile = kTileKeys * kRow; // one head's K (or V) tile
     static constexpr int kSlots = 2 * kSteps;      // MFMA slots of the tile step (QK^T and P.V alternate)
+    static constexpr int kPartRow = D == 128 ? 256 : 128;        // LDS row of one part
+    static constexpr int kParts = kRow / kPartRow;               // parts per tile
+    static constexpr int kPartBytes = kTileKeys * kPartRow;
+    static constexpr int kPartChunks = kPartRow / 16;            // 16-byte chunks per part row
+    static constexpr int kWaves = D == 256 ? 4 : 8;              // waves per workgroup
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kHalves = 8 / kWaves;                   // workgroups per work item
     static __device__ __forceinline__ int k_swizzle(int key) { return D == 128 ? (key & 15) : ((key >> 1) & 7); }
     static __device__ __forceinline__ int v_swizzle(int key) { return D == 128 ? 4 * (key & 3) : 4 * ((key >> 1) & 1); }
 };
@@ -150,6 +164,44 @@ template <bool B>
 struct NtTag {
     static constexpr bool value = B;
 };
+// A compile-time integer argument (a tile part).
+template <int N>
+struct IntTag {
+    static constexpr int value = N;
+};
+// f(0), f(1), ..., f(N - 1), each call with a constant argument.
+template <typename F, int... I>
+__device__ __forceinline__ void unrolled_seq(F&& f, std::integer_sequence<int, I...>) {
+    (f(I), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unrolled(F&& f) {
+    unrolled_seq(f, std::make_integer_sequence<int, N>{});
+}
+// Forms with an immediate byte offset (D = 256: the tile part).  The instruction adds its
+// immediate offset to the LDS address as well as to the global one, so M0 is set to the LDS
+// destination minus the offset.
+template <int OFS>
+__device__ __forceinline__ void dma_b128_o(const void* src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off offset:%2"
+                 :
+                 : "s"(lds_addr - OFS), "v"(src), "i"(OFS)
+                 : "memory", "m0");
+}
+template <int OFS>
+__device__ __forceinline__ void dma_b128_s_o(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3"
+                 :
+                 : "s"(lds_addr - OFS), "v"(lane_offset), "s"(base), "i"(OFS)
+                 : "memory", "m0");
+}
+template <int OFS>
+__device__ __forceinline__ void dma_b128_s_nt_o(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 offset:%3 nt"
+                 :
+                 : "s"(lds_addr - OFS), "v"(lane_offset), "s"(base), "i"(OFS)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ void dma_b32_s(uint32_t lane_offset, const void* base, uint32_t lds_addr) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                  :
@@ -189,39 +241,52 @@ constexpr int kReadAhead = 4;
 // operand-type rounding of the remainder, and both are multiplied into O (two MFMAs), with
 // the row sums taken in fp32; otherwise the probability is rounded to the operand type once.
 template <typename T, int HPW, bool EXACT, int G, int D>
-__device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it) {
+__device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const Item& it, const int half) {
     typedef HeadDim<D> HD;
     typedef typename Mfma<T>::vec V8;
     typedef typename Mfma<T>::pair V2;
     typedef __attribute__((address_space(3))) char lds_char;
-    constexpr int WPH = 8 / HPW;                        // waves per KV head
+    constexpr int THREADS = HD::kThreads;
+    constexpr int WPH = 8 / HPW;                        // waves per KV head (of the item's 8)
     constexpr int NW = 32 / G;                          // nodes per wave (G query heads each)
-    constexpr int NPW = NW * WPH;                       // nodes per workgroup
+    constexpr int NPW = NW * WPH;                       // nodes per work item
     static_assert(G >= 1 && G <= 16, "query heads per KV head");
+    // KV heads this workgroup stages: the item's HPW, or one per 4-wave half at D = 256 (a
+    // two-head item's halves are its two heads; a one-head item's halves share its head).
+    constexpr int HPWL = D == 256 ? 1 : HPW;
     // LDS ring of NS stages.  K tiles, V tiles and ancestor words live in three regions
     // so every operand address is a per-lane constant plus a compile-time stage offset.
-    constexpr int NS = HPW == 1 ? 8 : 4;
-    constexpr int TILE_SET = HPW * HD::kTile;           // K (or V) of the HPW heads, one stage
+    constexpr int NS = (HPWL == 1 && D != 256) ? 8 : 4;
+    constexpr int TILE_SET = HPWL * HD::kTile;          // K (or V) of the staged heads, one stage
     constexpr int V_REGION = NS * TILE_SET;
     constexpr int M_REGION = 2 * NS * TILE_SET;
     // DMA loads per tile per wave, at least: a K and a V load per head at D = 128 (each wave
-    // moves 4 keys, 16 lanes per key); at D = 64 waves 0-3 move K and waves 4-7 V, 8 keys each.
-    constexpr int LPT = D == 128 ? 2 * HPW : HPW;
+    // moves 4 keys, 16 lanes per key); at D = 64 waves 0-3 move K and waves 4-7 V, 8 keys each;
+    // at D = 256 each wave moves 8 keys of K and of V, one load per part.
+    constexpr int LPT = D == 128 ? 2 * HPW : (D == 64 ? HPW : 2 * HD::kParts);
     static_assert(M_REGION + NS * kMaskBytes <= kRingBytes, "ring exceeds its LDS region");
 
     // `wave` is the same in all lanes; readfirstlane lets the compiler see that, so
     // every per-wave quantity below lives in SGPRs and per-wave branches are scalar.
+    // `vw` is the wave's place among the item's 8 (the workgroup's half at D = 256).
     const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, g = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int hl = wave / WPH;
+    const int vw = D == 256 ? HD::kWaves * half + wave : wave;
+    const int hl = vw / WPH;
     const int head = it.h0 + hl;
-    const int nsub = wave - hl * WPH;
+    const int hs = D == 256 ? 0 : hl;                   // the head's place in the staged set
+    const int nsub = vw - hl * WPH;
     const int r = it.r;
     const int tn = p.cnt[r], qbase = p.cu[r], plen = p.plen[r];
     const int node = it.n0 + NW * nsub + c / G;
     const int qh = head * G + c % G;
     const bool head_ok = head < p.num_kv_heads;
     const bool wave_active = head_ok && (it.n0 + NW * nsub) < tn;
+    if constexpr (D == 256) {
+        // A half with no rows to compute (past the tree or the last head) stages nothing.
+        const int vw0 = HD::kWaves * half, hl0 = vw0 / WPH;
+        if (!(it.h0 + hl0 < p.num_kv_heads && it.n0 + NW * (vw0 - hl0 * WPH) < tn)) return;
+    }
     // Rows past NW * G (G not dividing 32) are padding: they load no Q and store nothing.
     const bool row_ok = head_ok && c < NW * G && node < tn;
     const int tree_end = (it.flags & kItemLastChunk) ? min(tn, it.n0 + NPW) : 0;
@@ -247,19 +312,26 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // this lane's Q rows into registers.  All of them are loaded before any is used
     // (at most one page and two slots per thread), so the three lookups cost one round
     // trip, not three.
-    static_assert(kMaxPages <= kThreads && kMaxTreeSlots <= 2 * kThreads, "one pass of page and slot loads");
-    static_assert(kMaxSlotChunk <= 4 * kThreads, "one pass of prefix slot loads");
+    constexpr int PPT = (kMaxPages + THREADS - 1) / THREADS;       // page loads per thread
+    constexpr int TPT = (kMaxTreeSlots + THREADS - 1) / THREADS;   // tree slot loads per thread
+    constexpr int SPT = (kMaxSlotChunk + THREADS - 1) / THREADS;   // prefix slot loads per thread
     int32_t* pages = reinterpret_cast<int32_t*>(smem + kPagesOffset);
     int32_t* tslots = reinterpret_cast<int32_t*>(smem + kSlotsOffset);
-    int32_t pg = 0;
-    int64_t sl[2] = {0, 0};
-    int64_t ps[4] = {0, 0, 0, 0};
-    if (tid < npages) pg = p.tables[static_cast<int64_t>(r) * p.t_s0 + page0 + tid];
+    int32_t pg[PPT];
+    int64_t sl[TPT];
+    int64_t ps[SPT];
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+        pg[k] = 0;
+        if (tid + k * THREADS < npages) pg[k] = p.tables[static_cast<int64_t>(r) * p.t_s0 + page0 + tid + k * THREADS];
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) ps[k] = 0;
     if (slot_mode) {
         const int64_t base = static_cast<int64_t>(r) * p.ps_s0 + it.kbeg;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = tid + k * kThreads;
+        for (int k = 0; k < SPT; ++k) {
+            const int i = tid + k * THREADS;
             if (i < nkeys) {
                 ps[k] = p.ps_i64 ? static_cast<const int64_t*>(p.pslots)[base + i]
                                  : static_cast<int64_t>(static_cast<const int32_t*>(p.pslots)[base + i]);
@@ -267,8 +339,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         }
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        if (tid + k * kThreads < tree_end) sl[k] = p.tree_slots[qbase + tid + k * kThreads];
+    for (int k = 0; k < TPT; ++k) {
+        sl[k] = 0;
+        if (tid + k * THREADS < tree_end) sl[k] = p.tree_slots[qbase + tid + k * THREADS];
     }
     // Q^T operand: lane (c, g) holds score row c, dims 16*st + 8*g + 0..7.
     V8 qb[HD::kSteps];
@@ -282,17 +355,21 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             qb[st] = __builtin_bit_cast(V8, raw);
         }
     }
-    if (tid < npages) {
-        if (pg < 0 || pg >= p.num_blocks) {
-            set_status(p.status, TV_STATUS_BAD_PAGE);
-            pg = 0;
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+        if (tid + k * THREADS < npages) {
+            int32_t v = pg[k];
+            if (v < 0 || v >= p.num_blocks) {
+                set_status(p.status, TV_STATUS_BAD_PAGE);
+                v = 0;
+            }
+            pages[tid + k * THREADS] = v;
         }
-        pages[tid] = pg;
     }
     if (slot_mode) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = tid + k * kThreads;
+        for (int k = 0; k < SPT; ++k) {
+            const int i = tid + k * THREADS;
             if (i < nkeys) {
                 int64_t v = ps[k];
                 if (v < 0 || v >= pool_slots) {
@@ -304,8 +381,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         }
     }
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int i = tid + k * kThreads;
+    for (int k = 0; k < TPT; ++k) {
+        const int i = tid + k * THREADS;
         if (i < tree_end) {
             int64_t v = sl[k];
             if (v < 0 || v >= pool_slots) {
@@ -322,12 +399,16 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
 
     lds_char* lds = (lds_char*)(smem);
     // Per-lane LDS operand offsets (stage 0).
-    //   K, MFMA step st: key c, chunk 2*st+g at position (2*st+g) ^ (c%16).
-    //   V, output block db: key vk (+16*kk+8*h), chunk 4*db+vc at position ^ 4*(vk%4).
+    //   K, MFMA step st: key c, chunk 2*st+g at position (2*st+g) ^ swizzle(c), in part
+    //   st / (steps per part).
+    //   V, output block db: key vk (+16*kk+8*h), chunk 4*db+vc at position ^ swizzle(vk), in
+    //   part db / (blocks per part).
+    constexpr int SPP = HD::kSteps / HD::kParts, BPP = HD::kBlocks / HD::kParts;
     uint32_t k_ofs[HD::kSteps];
 #pragma unroll
     for (int st = 0; st < HD::kSteps; ++st) {
-        k_ofs[st] = hl * HD::kTile + c * HD::kRow + (((2 * st + g) ^ HD::k_swizzle(c)) & (HD::kChunks - 1)) * 16;
+        k_ofs[st] = hs * HD::kTile + (st / SPP) * HD::kPartBytes + c * HD::kPartRow +
+                    (((2 * (st % SPP) + g) ^ HD::k_swizzle(c)) & (HD::kPartChunks - 1)) * 16;
     }
     const int grp = lane >> 4, src = lane & 15;
     const int vk = 4 * (grp >> 1) + (src >> 2);
@@ -335,8 +416,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     uint32_t v_ofs[HD::kBlocks];
 #pragma unroll
     for (int db = 0; db < HD::kBlocks; ++db) {
-        v_ofs[db] = V_REGION + hl * HD::kTile + vk * HD::kRow +
-                    (((4 * db + vc) ^ HD::v_swizzle(vk)) & (HD::kChunks - 1)) * 16 + (src & 1) * 8;
+        v_ofs[db] = V_REGION + hs * HD::kTile + (db / BPP) * HD::kPartBytes + vk * HD::kPartRow +
+                    (((4 * (db % BPP) + vc) ^ HD::v_swizzle(vk)) & (HD::kPartChunks - 1)) * 16 + (src & 1) * 8;
     }
     const uint32_t m_ofs = M_REGION + wave * 256 + 4 * (c / G);
 
@@ -347,11 +428,13 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // per-lane 64-bit address: for a prefix tile the tile's page base (scalar
     // arithmetic) plus a per-lane byte offset, for a tree tile the lane's own slot.
     // At D = 128 wave w moves keys 4w..4w+3 of every tile (16 lanes per key); at D = 64 wave w
-    // moves keys 8(w%4)..8(w%4)+7 (8 lanes per key) of K (w < 4) or V (w >= 4).
+    // moves keys 8(w%4)..8(w%4)+7 (8 lanes per key) of K (w < 4) or V (w >= 4); at D = 256
+    // (4 waves) wave w moves keys 8w..8w+7 of K and of V, one load per part (8 lanes per key,
+    // the part's 8 chunks; part p adds 128p bytes to the global address and 4 KiB in LDS).
     const int s_key = D == 128 ? (tid >> 4) : 8 * (wave & 3) + (lane >> 3);
-    const int k_chunk = (lane & (HD::kChunks - 1)) ^ HD::k_swizzle(s_key);
-    const int v_chunk = (lane & (HD::kChunks - 1)) ^ HD::v_swizzle(s_key);
-    const bool k_wave = D == 128 || wave < 4;   // D = 64: this wave's DMA moves K (else V)
+    const int k_chunk = (lane & (HD::kPartChunks - 1)) ^ HD::k_swizzle(s_key);
+    const int v_chunk = (lane & (HD::kPartChunks - 1)) ^ HD::v_swizzle(s_key);
+    const bool k_wave = D != 64 || wave < 4;    // D = 64: this wave's DMA moves K (else V)
     const uint32_t k_chunk_b = 16u * k_chunk, v_chunk_b = 16u * v_chunk;
     // Byte strides; the host checks that a page stride fits 32 bits and 32 key rows 31.
     const uint32_t k_page_b = static_cast<uint32_t>(p.k_s0 * static_cast<int64_t>(sizeof(T)));
@@ -360,14 +443,16 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const uint32_t v_key_b = static_cast<uint32_t>(p.v_s1 * static_cast<int64_t>(sizeof(T)));
     const uint32_t k_lane_b = s_key * k_key_b + k_chunk_b;
     const uint32_t v_lane_b = s_key * v_key_b + v_chunk_b;
-    // Head h0 of the group, and the byte step to head h0 + j (clamped to the last head).
-    const int h0c = min(it.h0, p.num_kv_heads - 1);
+    // First staged head (h0 of the group; at D = 256 the half's head), and the byte step to
+    // staged head j (clamped to the last head).
+    const int hfirst = D == 256 && HPW == 2 ? it.h0 + half : it.h0;
+    const int h0c = min(hfirst, p.num_kv_heads - 1);
     const uint64_t k_head_b = reinterpret_cast<uint64_t>(p.k) + static_cast<uint64_t>(h0c * p.k_s2 * sizeof(T));
     const uint64_t v_head_b = reinterpret_cast<uint64_t>(p.v) + static_cast<uint64_t>(h0c * p.v_s2 * sizeof(T));
-    int64_t k_hstep_b[HPW], v_hstep_b[HPW];
+    int64_t k_hstep_b[HPWL], v_hstep_b[HPWL];
 #pragma unroll
-    for (int j = 0; j < HPW; ++j) {
-        const int64_t dh = min(it.h0 + j, p.num_kv_heads - 1) - h0c;
+    for (int j = 0; j < HPWL; ++j) {
+        const int64_t dh = min(hfirst + j, p.num_kv_heads - 1) - h0c;
         k_hstep_b[j] = dh * p.k_s2 * static_cast<int64_t>(sizeof(T));
         v_hstep_b[j] = dh * p.v_s2 * static_cast<int64_t>(sizeof(T));
     }
@@ -476,11 +561,30 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         const uint64_t src = k_wave ? dk + k_hstep_b[j] : dv + v_hstep_b[j];
         dma_b128(reinterpret_cast<const void*>(src), tile_dst(stage * TILE_SET + j * HD::kTile));
     };
+    // D = 256: part P of this wave's K (or V) keys of the staged head.
+    auto issue_k_part = [&](auto part, int stage) {
+        constexpr int P = decltype(part)::value;
+        dma_b128_o<128 * P>(reinterpret_cast<const void*>(dk), tile_dst(stage * TILE_SET + P * HD::kPartBytes));
+    };
+    auto issue_v_part = [&](auto part, int stage) {
+        constexpr int P = decltype(part)::value;
+        dma_b128_o<128 * P>(reinterpret_cast<const void*>(dv),
+                            tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
+    };
     auto issue_mask = [&](int stage) {
         if (dtree) dma_b32_s(m_lane_b, uniform_ptr(anc_req + dmask), mask_dst(stage * kMaskBytes));
     };
     auto issue_all = [&](int stage) {
-        if constexpr (D == 128) {
+        if constexpr (D == 256) {
+            issue_k_part(IntTag<0>{}, stage);
+            issue_k_part(IntTag<1>{}, stage);
+            issue_k_part(IntTag<2>{}, stage);
+            issue_k_part(IntTag<3>{}, stage);
+            issue_v_part(IntTag<0>{}, stage);
+            issue_v_part(IntTag<1>{}, stage);
+            issue_v_part(IntTag<2>{}, stage);
+            issue_v_part(IntTag<3>{}, stage);
+        } else if constexpr (D == 128) {
 #pragma unroll
             for (int j = 0; j < HPW; ++j) issue_k(stage, j);
 #pragma unroll
@@ -594,9 +698,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         auto vread = [&](int j) {
             const int kk = j / HD::kBlocks, db = j % HD::kBlocks;
             vlo[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * HD::kRow));
+                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * HD::kPartRow));
             vhi[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * HD::kRow));
+                (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * HD::kPartRow));
         };
         auto slot_mfma = [&](int sl) {
             if ((sl & 1) == 0) {
@@ -642,8 +746,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
 #pragma unroll
         for (int sl = 0; sl < kReadAhead; ++sl) slot_read(sl);
         order_point();
-#pragma unroll
-        for (int sl = 0; sl < HD::kSlots; ++sl) {
+        auto slot = [&](int sl) {
             if (sl == HD::kSlots / 2) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) ex(e);
@@ -658,6 +761,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             order_point();
             piece(sl);
             order_point();
+        };
+        if constexpr (D == 256) {
+            // 32 slots exceed the unroller's size limit for a pragma; a fold over the slot
+            // indices unrolls them at compile time.
+            unrolled<HD::kSlots>(slot);
+        } else {
+#pragma unroll
+            for (int sl = 0; sl < HD::kSlots; ++sl) slot(sl);
         }
         return l0 + l1;
     };
@@ -676,7 +787,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         // make that stage's V finite.
         typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 #pragma unroll
-        for (int i = tid; i < TILE_SET / 16; i += kThreads) {
+        for (int i = tid; i < TILE_SET / 16; i += THREADS) {
             *(lds_u32x4*)(lds + V_REGION + (NS - 1) * TILE_SET + 16 * i) = u32x4{0u, 0u, 0u, 0u};
         }
     }
@@ -699,9 +810,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     const uint32_t k_tile_b = kTileKeys * k_key_b, v_tile_b = kTileKeys * v_key_b;
     const uint64_t k_head_u = reinterpret_cast<uint64_t>(uniform_ptr(reinterpret_cast<const void*>(k_head_b)));
     const uint64_t v_head_u = reinterpret_cast<uint64_t>(uniform_ptr(reinterpret_cast<const void*>(v_head_b)));
-    uint32_t k_lane_h[HPW], v_lane_h[HPW], kv_lane_h[HPW];
+    uint32_t k_lane_h[HPWL], v_lane_h[HPWL], kv_lane_h[HPWL];
 #pragma unroll
-    for (int j = 0; j < HPW; ++j) {
+    for (int j = 0; j < HPWL; ++j) {
         k_lane_h[j] = k_lane_b + static_cast<uint32_t>(k_hstep_b[j]);
         v_lane_h[j] = v_lane_b + static_cast<uint32_t>(v_hstep_b[j]);
         kv_lane_h[j] = k_wave ? k_lane_h[j] : v_lane_h[j];
@@ -731,6 +842,27 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         } else {
             dma_b128_s(v_lane_h[j], reinterpret_cast<const void*>(fv),
                        tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
+        }
+    };
+    // D = 256: part P of this wave's streamed K (or V) keys.
+    auto fast_issue_k_part = [&](auto nt, auto part, int stage) {
+        constexpr int P = decltype(part)::value;
+        if constexpr (decltype(nt)::value) {
+            dma_b128_s_nt_o<128 * P>(k_lane_h[0], reinterpret_cast<const void*>(fk),
+                                     tile_dst(stage * TILE_SET + P * HD::kPartBytes));
+        } else {
+            dma_b128_s_o<128 * P>(k_lane_h[0], reinterpret_cast<const void*>(fk),
+                                  tile_dst(stage * TILE_SET + P * HD::kPartBytes));
+        }
+    };
+    auto fast_issue_v_part = [&](auto nt, auto part, int stage) {
+        constexpr int P = decltype(part)::value;
+        if constexpr (decltype(nt)::value) {
+            dma_b128_s_nt_o<128 * P>(v_lane_h[0], reinterpret_cast<const void*>(fv),
+                                     tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
+        } else {
+            dma_b128_s_o<128 * P>(v_lane_h[0], reinterpret_cast<const void*>(fv),
+                                  tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
         }
     };
     // D = 64: this wave's one streamed load per head and tile, K or V.
@@ -804,7 +936,17 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     __syncthreads();
                     const int ds = (b + NS - 2) % NS;
                     auto piece = [&](int sl) {
-                        if constexpr (D == 128) {
+                        if constexpr (D == 256) {
+                            if (sl == 2) fast_issue_k_part(nt, IntTag<0>{}, ds);
+                            if (sl == 4) fast_issue_k_part(nt, IntTag<1>{}, ds);
+                            if (sl == 6) fast_issue_k_part(nt, IntTag<2>{}, ds);
+                            if (sl == 8) fast_issue_k_part(nt, IntTag<3>{}, ds);
+                            if (sl == 10) fast_issue_v_part(nt, IntTag<0>{}, ds);
+                            if (sl == 12) fast_issue_v_part(nt, IntTag<1>{}, ds);
+                            if (sl == 14) fast_issue_v_part(nt, IntTag<2>{}, ds);
+                            if (sl == 18) fast_issue_v_part(nt, IntTag<3>{}, ds);
+                            if (sl == 24) fast_advance();
+                        } else if constexpr (D == 128) {
                             if (HPW == 1) {
                                 if (sl == 4) fast_issue_k(nt, ds, 0);
                                 if (sl == 8) fast_issue_v(nt, ds, 0);
@@ -847,7 +989,16 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     wait_vmcnt<(NS - 4) * LPT>();
                     __syncthreads();
                     const int ds = (b + NS - 2) % NS;
-                    if constexpr (D == 128) {
+                    if constexpr (D == 256) {
+                        fast_issue_k_part(nt, IntTag<0>{}, ds);
+                        fast_issue_k_part(nt, IntTag<1>{}, ds);
+                        fast_issue_k_part(nt, IntTag<2>{}, ds);
+                        fast_issue_k_part(nt, IntTag<3>{}, ds);
+                        fast_issue_v_part(nt, IntTag<0>{}, ds);
+                        fast_issue_v_part(nt, IntTag<1>{}, ds);
+                        fast_issue_v_part(nt, IntTag<2>{}, ds);
+                        fast_issue_v_part(nt, IntTag<3>{}, ds);
+                    } else if constexpr (D == 128) {
 #pragma unroll
                         for (int j = 0; j < HPW; ++j) fast_issue_k(nt, ds, j);
 #pragma unroll
@@ -861,8 +1012,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             }
         }
     };
-    if (!EXACT && tn <= NPW && t_fast >= 64) {
-        fast_steps(NtTag<!EXACT>{});
+    // D = 256 keeps the cacheable form only: a one-head item's two halves read one K/V stream,
+    // and two forms of its loop do not fit the registers.
+    if (!EXACT && D != 256 && tn <= NPW && t_fast >= 64) {
+        fast_steps(NtTag<!EXACT && D != 256>{});
     } else {
         fast_steps(NtTag<false>{});
     }
@@ -880,7 +1033,18 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             const int ds = (b + NS - 2) % NS;
             auto piece = [&](int sl) {
                 if (sl == 1) describe(t + NS - 2, pf);
-                if constexpr (D == 128) {
+                if constexpr (D == 256) {
+                    if (sl == 3) issue_k_part(IntTag<0>{}, ds);
+                    if (sl == 5) issue_k_part(IntTag<1>{}, ds);
+                    if (sl == 7) issue_k_part(IntTag<2>{}, ds);
+                    if (sl == 9) issue_k_part(IntTag<3>{}, ds);
+                    if (sl == 11) issue_v_part(IntTag<0>{}, ds);
+                    if (sl == 13) issue_v_part(IntTag<1>{}, ds);
+                    if (sl == 15) issue_v_part(IntTag<2>{}, ds);
+                    if (sl == 17) issue_v_part(IntTag<3>{}, ds);
+                    if (sl == 20) issue_mask(ds);
+                    if (sl == 22) pf = fetch(t + NS - 1);
+                } else if constexpr (D == 128) {
                     if (HPW == 1) {
                         if (sl == 4) issue_k(ds, 0);
                         if (sl == 8) issue_v(ds, 0);
@@ -929,9 +1093,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
 #pragma unroll
             for (int db = 0; db < HD::kBlocks; ++db) {
                 const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * HD::kRow));
+                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk) * HD::kPartRow));
                 const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * HD::kRow));
+                    (lds_i16x4*)(lds + v_ofs[db] + vst + (16 * kk + 8) * HD::kPartRow));
                 const V8 a = __builtin_bit_cast(V8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[db] = Mfma<T>::run(a, pb_prev[kk], acc[db]);
                 if constexpr (EXACT) acc[db] = Mfma<T>::run(a, pl_prev[kk], acc[db]);
@@ -943,7 +1107,7 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     if (!wave_active) return;
     l_run += __shfl_xor(l_run, 32);  // both halves of the row
     if (!row_ok) return;
-    const int wr = wave * 32 + c;  // score row within the item
+    const int wr = vw * 32 + c;  // score row within the item
     if (it.slot < 0) {
         const float inv = 1.f / l_run;
         const int64_t row = qbase + node;
@@ -972,16 +1136,27 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
 }
 
 template <typename T, bool EXACT, int G, int D>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(HeadDim<D>::kThreads)
 tree_attention_kernel(const AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+    // D = 256: two 4-wave workgroups per work item.  Item i's halves are workgroups
+    // 16 * (i / 8) + i % 8 and that + 8: both on XCD i % 8 (workgroup w runs on XCD w % 8),
+    // where the planner placed the item, and dispatched close together, so a one-head item's
+    // halves share its K/V stream in that XCD's L2.
+    int item = static_cast<int>(blockIdx.x), half = 0;
+    if constexpr (D == 256) {
+        item = (item >> 4) * 8 + (item & 7);
+        half = (static_cast<int>(blockIdx.x) >> 3) & 1;
+    }
     // A device-built plan launches a capacity grid; workgroups past its item count exit.
     // A plan that overflowed its capacities has no items and reports it here.
     if (p.counts) {
         if (p.counts[3] != 0 && blockIdx.x == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
-        if (static_cast<int>(blockIdx.x) >= p.counts[0]) return;
+        if (item >= p.counts[0]) return;
+    } else if (D == 256 && item >= p.num_items) {
+        return;
     }
-    const int32_t* d = p.items + 8 * blockIdx.x;
+    const int32_t* d = p.items + 8 * static_cast<int64_t>(item);
     const Item it{d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7]};
     if (it.r < 0 || it.r >= p.num_requests) {
         if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
@@ -1009,8 +1184,8 @@ tree_attention_kernel(const AttnParams p) {
         }
     }
     switch (it.hpw) {
-        case 1: run_item<T, 1, EXACT, G, D>(p, smem, it); break;
-        case 2: run_item<T, 2, EXACT, G, D>(p, smem, it); break;
+        case 1: run_item<T, 1, EXACT, G, D>(p, smem, it, half); break;
+        case 2: run_item<T, 2, EXACT, G, D>(p, smem, it, half); break;
         default:
             if (threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
             break;
@@ -1019,17 +1194,20 @@ tree_attention_kernel(const AttnParams p) {
 
 template <int G, int D = 128>
 int launch_group(const AttnParams& p, int32_t num_items, bool bf16, bool exact, hipStream_t s) {
+    typedef HeadDim<D> HD;
+    // D = 256: both halves of every item, on a grid of whole 16-workgroup windows.
+    const uint32_t grid = D == 256 ? static_cast<uint32_t>((num_items + 7) / 8) * 16u : static_cast<uint32_t>(num_items);
     if (bf16) {
         if (exact) {
-            hipLaunchKernelGGL((tree_attention_kernel<__bf16, true, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<__bf16, true, G, D>), dim3(grid), dim3(HD::kThreads), 0, s, p);
         } else {
-            hipLaunchKernelGGL((tree_attention_kernel<__bf16, false, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<__bf16, false, G, D>), dim3(grid), dim3(HD::kThreads), 0, s, p);
         }
     } else {
         if (exact) {
-            hipLaunchKernelGGL((tree_attention_kernel<_Float16, true, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<_Float16, true, G, D>), dim3(grid), dim3(HD::kThreads), 0, s, p);
         } else {
-            hipLaunchKernelGGL((tree_attention_kernel<_Float16, false, G, D>), dim3(num_items), dim3(kThreads), 0, s, p);
+            hipLaunchKernelGGL((tree_attention_kernel<_Float16, false, G, D>), dim3(grid), dim3(HD::kThreads), 0, s, p);
         }
     }
     return TV_OK;   // the caller reads the launch status (check_launch)

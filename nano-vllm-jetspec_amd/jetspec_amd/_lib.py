@@ -58,6 +58,7 @@ EXPORTED_SYMBOLS = (
     "tv_stream_capture_info",
     "tv_tree_attention_noalloc",
     "tv_tree_attention_noalloc_max_workspace",
+    "tv_tree_attention_workspace_bytes",
     "tv_tree_attention_fp32",
     "tv_sizeof_tree_attention_fp32_args",
 )
@@ -221,6 +222,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tv_tree_attention_noalloc.argtypes = [POINTER(TreeAttentionArgs), c_void_p]
     lib.tv_tree_attention_noalloc_max_workspace.restype = c_int64
     lib.tv_tree_attention_noalloc_max_workspace.argtypes = []
+    lib.tv_tree_attention_workspace_bytes.restype = c_int64
+    lib.tv_tree_attention_workspace_bytes.argtypes = [c_int32, c_int32]
     lib.tv_tree_attention_fp32.restype = c_int32
     lib.tv_tree_attention_fp32.argtypes = [POINTER(TreeAttentionFp32Args), c_void_p]
     lib.tv_sizeof_tree_attention_fp32_args.restype = c_int64

@@ -63,13 +63,23 @@ _BACKENDS = ("auto", "reference", "prefix", "gqa")
 # powers of two up to 16, tree_gqa.py:124-126; 3, 5, 6 and 7 are the GQA ratios of other
 # Qwen-family checkpoints, e.g. 40 query over 8 KV heads).  Other ratios run the FP32 kernel.
 SUPPORTED_GROUPS = (1, 2, 3, 4, 5, 6, 7, 8, 16)
-# Head size 64 runs the MFMA kernel for the power-of-two groups of the reference's grouped kernel.
+# Head sizes 64 and 256 run the MFMA kernel for the power-of-two groups of the reference's grouped
+# kernel (tree_gqa.py:124-135).
 SUPPORTED_GROUPS_D64 = (1, 2, 4, 8, 16)
+SUPPORTED_GROUPS_D256 = (1, 2, 4, 8, 16)
 
 
 def mfma_head(head_size: int, groups: int) -> bool:
     """Head size and query group the MFMA kernel is built for."""
-    return (head_size == 128 and groups in SUPPORTED_GROUPS) or (head_size == 64 and groups in SUPPORTED_GROUPS_D64)
+    return ((head_size == 128 and groups in SUPPORTED_GROUPS) or (head_size == 64 and groups in SUPPORTED_GROUPS_D64)
+            or (head_size == 256 and groups in SUPPORTED_GROUPS_D256))
+
+
+def workspace_bytes(plan_bytes: int, partial_slots: int, head_dim: int) -> int:
+    """Split-prefix workspace of a plan at this head size (a plan's own figure holds up to 128)."""
+    if not partial_slots:
+        return int(plan_bytes)
+    return max(int(plan_bytes), int(_lib.library().tv_tree_attention_workspace_bytes(partial_slots, head_dim)))
 
 
 _FP32_ROUTE = "fp32"     # cache entries of batches that run the FP32 kernel
@@ -302,14 +312,15 @@ def _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads: int, queri
     state = derived_state(metadata, num_kv_heads, queries_per_kv=queries_per_kv, chunk_keys=chunk_keys)
     device = k_pool.device
     workspace = None
-    if state["workspace_bytes"]:
+    ws_bytes = workspace_bytes(state["workspace_bytes"], state["num_partial_slots"], int(k_pool.shape[3]))
+    if ws_bytes:
         # One workspace per plan and stream: launches on one stream run in order, so the
         # per-layer launches of a round reuse it (each merge finishes before the next
         # layer's attention writes its partials).
-        ws_key = ("workspace", num_kv_heads, queries_per_kv, chunk_keys, stream)
+        ws_key = ("workspace", num_kv_heads, queries_per_kv, chunk_keys, stream, ws_bytes)
         workspace = per_meta.get(ws_key)
         if workspace is None:
-            workspace = per_meta[ws_key] = torch.empty(state["workspace_bytes"], dtype=torch.uint8, device=device)
+            workspace = per_meta[ws_key] = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     a = _lib.TreeAttentionArgs()
     fill_pool_args(a, metadata, k_pool, v_pool, num_kv_heads, queries_per_kv, _device.status_word(device))
     a.ancestor_words = state["ancestor_words"].data_ptr()
@@ -320,7 +331,7 @@ def _eager_template(per_meta, metadata, k_pool, v_pool, num_kv_heads: int, queri
     a.num_groups = state["num_groups"]
     a.num_partial_slots = state["num_partial_slots"]
     a.workspace = workspace.data_ptr() if workspace is not None else None
-    a.workspace_bytes = state["workspace_bytes"]
+    a.workspace_bytes = ws_bytes
     a.device_counts = None
     # Keep every buffer the block points at alive as long as the block.
     return a, (state["ancestor_words"], state["items_dev"], state["groups_dev"], workspace)
@@ -343,11 +354,12 @@ def _launch_captured(q, k_pool, v_pool, metadata, scale, out, num_kv_heads: int,
     from .target_graph import GraphedTreeAttention
 
     per_meta = _per_metadata(metadata)
-    key = ("graph", num_kv_heads, queries_per_kv, chunk_keys)
+    head_dim = int(k_pool.shape[3])
+    key = ("graph", num_kv_heads, queries_per_kv, chunk_keys, head_dim)
     graphed = per_meta.get(key)
     if graphed is None:
         graphed = per_meta[key] = GraphedTreeAttention.for_signature(
-            metadata, num_kv_heads, queries_per_kv=queries_per_kv, chunk_keys=chunk_keys)
+            metadata, num_kv_heads, queries_per_kv=queries_per_kv, chunk_keys=chunk_keys, head_dim=head_dim)
     capture = _capture_id(stream)
     if graphed.prepared_capture != capture:
         graphed.prepare(metadata)   # recorded once at the head of this graph's sequence
@@ -578,7 +590,8 @@ def _legacy_mfma(q, k_pool, v_pool, req, scale, num_queries_per_kv: int, block_s
         ctypes.byref(info)), "tree_attention_plan_slots")
     items_dev = torch.from_numpy(items).to(device)
     groups_dev = torch.from_numpy(groups).to(device)
-    workspace = torch.empty(max(int(info.workspace_bytes), 1), dtype=torch.uint8, device=device)
+    ws_bytes = workspace_bytes(info.workspace_bytes, info.num_partial_slots, int(q.shape[2]))
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
         q = q.contiguous()
     a = _lib.TreeAttentionArgs()
@@ -613,8 +626,8 @@ def _legacy_mfma(q, k_pool, v_pool, req, scale, num_queries_per_kv: int, block_s
     a.groups = groups_dev.data_ptr() if info.num_groups else None
     a.num_groups = info.num_groups
     a.num_partial_slots = info.num_partial_slots
-    a.workspace = workspace.data_ptr() if info.workspace_bytes else None
-    a.workspace_bytes = int(info.workspace_bytes)
+    a.workspace = workspace.data_ptr() if ws_bytes else None
+    a.workspace_bytes = ws_bytes
     a.status = status.data_ptr()
     a.prefix_slots = req.slots.data_ptr()
     a.prefix_slots_stride = 0

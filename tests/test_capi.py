@@ -132,9 +132,10 @@ def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
                 (256 * 256, 256, 1 << 30, 1)):  # next KV head 2 GiB away
         assert lib.tv_tree_attention(ctypes.byref(args(bad)), None) == _lib.TV_ERR_UNSUPPORTED, bad
         assert b"strides out of range" in lib.tv_last_error()
-    # Head sizes: 128 for every group, 64 for the power-of-two groups; others take the FP32 entry.
+    # Head sizes: 128 for every group, 64 and 256 for the power-of-two groups; others take the
+    # FP32 entry.
     for head, q_heads, accepted in ((64, 8, True), (64, 32, True), (64, 6, False), (96, 8, False),
-                                    (256, 8, False)):
+                                    (256, 8, True), (256, 32, True), (256, 6, False), (512, 8, False)):
         a = args((256 * 256, 256, 128, 1))
         a.head_dim, a.num_q_heads, a.num_requests = head, q_heads, 1
         code = lib.tv_tree_attention(ctypes.byref(a), None)
@@ -155,6 +156,44 @@ def test_attention_rejects_strides_beyond_its_32_bit_offsets_without_a_device():
         a.num_partial_slots, a.workspace, a.workspace_bytes = slots, workspace, 1 << 30
         assert lib.tv_tree_attention(ctypes.byref(a), None) == _lib.TV_ERR_INVALID, slots
         assert message in lib.tv_last_error()
+
+
+def test_split_workspace_follows_the_head_size():
+    """A plan's workspace_bytes holds head sizes up to 128; at 256 the partial rows are twice
+    as long, and tv_tree_attention refuses the plan's figure (TV_ERR_CAPACITY) until the
+    workspace is tv_tree_attention_workspace_bytes(slots, 256)."""
+    lib = _lib.library()
+    plan = make_plan([3000, 5000, 700], [40, 64, 17], 8, 256, 256, chunk_keys=512, queries_per_kv=4)
+    slots, ws = plan["num_partial_slots"], plan["workspace_bytes"]
+    assert slots > 0
+    for head in (64, 96, 128):
+        assert lib.tv_tree_attention_workspace_bytes(slots, head) == ws, head
+    rows = slots * 256
+    assert ws == -(-rows * 128 * 4 // 256) * 256 + -(-rows * 8 // 256) * 256
+    assert lib.tv_tree_attention_workspace_bytes(slots, 256) == -(-rows * 256 * 4 // 256) * 256 + -(-rows * 8 // 256) * 256
+    assert lib.tv_tree_attention_workspace_bytes(0, 256) == 0
+    a = _lib.TreeAttentionArgs()
+    a.q = a.k_pool = a.v_pool = a.out = 0x10000
+    a.q_stride_row, a.q_stride_head = 8 * 256, 256
+    a.out_stride_row, a.out_stride_head = 8 * 256, 256
+    for i in range(4):
+        a.k_stride[i] = a.v_stride[i] = (256 * 2 * 256, 2 * 256, 256, 1)[i]
+    a.in_dtype = a.out_dtype = _lib.TV_BF16
+    a.num_q_heads, a.num_kv_heads, a.head_dim, a.block_size = 8, 2, 256, 256
+    a.scale = 256 ** -0.5
+    a.ancestor_words_per_row = 1
+    a.num_blocks, a.num_requests, a.num_items, a.num_groups = 8, 1, 1, 1
+    a.cu_seqlens_q = a.prefix_lens = a.node_counts = a.block_tables = a.items = a.groups = 0x10000
+    a.tree_slots = a.ancestor_words = 0x10000
+    a.num_partial_slots, a.workspace, a.workspace_bytes = slots, 0x20000, ws
+    assert lib.tv_tree_attention(ctypes.byref(a), None) == _lib.TV_ERR_CAPACITY
+    assert b"workspace" in lib.tv_last_error()
+    # The built-in scratch of the allocation-free entry holds half as many slots at 256.
+    scratch = lib.tv_tree_attention_noalloc_max_workspace()
+    assert lib.tv_tree_attention_workspace_bytes(504, 128) <= scratch < lib.tv_tree_attention_workspace_bytes(505, 128)
+    assert lib.tv_tree_attention_workspace_bytes(254, 256) <= scratch < lib.tv_tree_attention_workspace_bytes(255, 256)
+    a.num_partial_slots = 255
+    assert lib.tv_tree_attention_noalloc(ctypes.byref(a), None) == _lib.TV_ERR_CAPACITY
 
 
 def nodes_per_item(hpw, groups):

@@ -99,7 +99,7 @@ def test_legacy_entry_rejections_before_any_device_work():
 
 def test_kernel_choice_follows_the_mfma_geometry():
     """The drop-in's per-batch kernel choice (host logic): the MFMA kernel for bf16/f16,
-    head_dim 128 with 1-8 or 16 query heads per KV head or head_dim 64 with 1, 2, 4, 8 or 16,
+    head_dim 128 with 1-8 or 16 query heads per KV head or head_dim 64 or 256 with 1, 2, 4, 8 or 16,
     page sizes that are multiples of 32, trees of at most 1024 nodes and 16-byte aligned K/V
     rows; the FP32 kernel otherwise."""
     from types import SimpleNamespace
@@ -120,11 +120,12 @@ def test_kernel_choice_follows_the_mfma_geometry():
     assert not case(dtype=torch.float32)
     for groups in (9, 12, 32):
         assert not case(groups=groups), groups
-    for groups in (1, 2, 4, 8, 16):
-        assert case(head_dim=64, groups=groups), groups
-    for groups in (3, 5, 6, 7):
-        assert not case(head_dim=64, groups=groups), groups
-    for head_dim in (32, 96, 256):
+    for head_dim in (64, 256):
+        for groups in (1, 2, 4, 8, 16):
+            assert case(head_dim=head_dim, groups=groups), (head_dim, groups)
+        for groups in (3, 5, 6, 7):
+            assert not case(head_dim=head_dim, groups=groups), (head_dim, groups)
+    for head_dim in (32, 96, 512):
         assert not case(head_dim=head_dim), head_dim
     assert not case(block=16) and not case(block=48)
     assert not case(nodes=(64, 1025))

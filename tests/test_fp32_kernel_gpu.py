@@ -103,19 +103,16 @@ def test_f32_operands_through_every_fp32_entry():
         packed_tree_attention(q, k, v, meta, scale, 4, backend="gqa")
 
 
-@pytest.mark.parametrize("head_dim,groups", [(64, 3), (96, 4), (256, 4), (512, 4)])
+@pytest.mark.parametrize("head_dim,groups", [(64, 3), (96, 4), (256, 3), (512, 4)])
 def test_head_sizes(head_dim, groups):
-    """Head sizes outside the MFMA kernel's (128 for every group, 64 for the power-of-two
-    groups, tests/test_head64_gpu.py)."""
+    """Head sizes outside the MFMA kernel's (128 for every group, 64 and 256 for the power-of-two
+    groups, tests/test_head64_gpu.py and tests/test_head256_gpu.py)."""
     q, k, v, meta, *_ = make_case((300, 0, 1025), (17, 40, 64), head_dim=head_dim, groups=groups, seed=head_dim)
     assert not _mfma_geometry(q, k, v, meta)
     scale = head_dim ** -0.5
     check(packed_tree_attention(q, k, v, meta, scale, groups), q, k, v, meta, f"D{head_dim} auto", scale=scale)
     check(packed_tree_attention(q, k, v, meta, scale, groups, output_dtype=torch.float32), q, k, v, meta,
           f"D{head_dim} f32 out", scale=scale)
-    if head_dim == 256:   # the grouped entry takes any head size as the reference's does
-        check(packed_tree_attention(q, k, v, meta, scale, 4, backend="gqa"), q, k, v, meta, f"D{head_dim} gqa",
-              scale=scale)
 
 
 @pytest.mark.parametrize("groups,kv_heads", [(9, 2), (12, 1), (32, 1)])
