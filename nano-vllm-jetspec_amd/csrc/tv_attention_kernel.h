@@ -256,7 +256,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     constexpr int HPWL = D == 256 ? 1 : HPW;
     // LDS ring of NS stages.  K tiles, V tiles and ancestor words live in three regions
     // so every operand address is a per-lane constant plus a compile-time stage offset.
-    constexpr int NS = (HPWL == 1 && D != 256) ? 8 : 4;
+    // 32 KiB tile sets (two heads at D = 128, one at D = 256) leave room for 4 stages.
+    constexpr int NS = (D == 256 || (D == 128 && HPWL == 2)) ? 4 : 8;
     constexpr int TILE_SET = HPWL * HD::kTile;          // K (or V) of the staged heads, one stage
     constexpr int V_REGION = NS * TILE_SET;
     constexpr int M_REGION = 2 * NS * TILE_SET;
@@ -265,6 +266,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // at D = 256 each wave moves 8 keys of K and of V, one load per part.
     constexpr int LPT = D == 128 ? 2 * HPW : (D == 64 ? HPW : 2 * HD::kParts);
     static_assert(M_REGION + NS * kMaskBytes <= kRingBytes, "ring exceeds its LDS region");
+    // A 4-stage ring stages K one tile further ahead than V (SPLIT): in step t, K of tile t+3
+    // goes into the stage of tile t-1, whose K was last read in step t-2 (its V is still read
+    // in step t), and V (with the ancestor words) of tile t+2 into the stage of tile t-2.  K
+    // then has two steps to arrive and V three, and each step waits only for the loads issued
+    // two steps back: two tile sets in flight per workgroup instead of one.
+    constexpr bool SPLIT = NS == 4;
+    constexpr int LPTK = D == 256 ? HD::kParts : HPW;   // K loads per tile and wave (SPLIT)
+    constexpr int WAIT_STEP = SPLIT ? LPT : (NS - 4) * LPT;   // loads a step may leave in flight
 
     // `wave` is the same in all lanes; readfirstlane lets the compiler see that, so
     // every per-wave quantity below lives in SGPRs and per-wave branches are scalar.
@@ -595,6 +604,18 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         }
         issue_mask(stage);
     };
+    // SPLIT rings (D = 128 two-head items, D = 256): the K or the V loads of a described tile.
+    auto issue_k_set = [&](int stage) {
+        if constexpr (D == 256) {
+            issue_k_part(IntTag<0>{}, stage);
+            issue_k_part(IntTag<1>{}, stage);
+            issue_k_part(IntTag<2>{}, stage);
+            issue_k_part(IntTag<3>{}, stage);
+        } else {
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) issue_k(stage, j);
+        }
+    };
     f32x16 acc[HD::kBlocks];
 #pragma unroll
     for (int db = 0; db < HD::kBlocks; ++db) acc[db] = f32x16{};
@@ -796,6 +817,10 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         describe(b, fetch(b));
         issue_all(b);
     }
+    if constexpr (SPLIT) {
+        describe(NS - 2, fetch(NS - 2));
+        issue_k_set(NS - 2);
+    }
 
     // Streaming DMA of whole prefix tiles.  Steps t < t_fast need no mask and stage a
     // whole prefix tile t+NS-2, so their loads come from wave-uniform K and V tile
@@ -803,8 +828,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // offset; a new page is read from the LDS page list, prefetched one page ahead,
     // when the current one is used up.  Pages hold whole tiles when B is a multiple
     // of the tile (the item's first key is).
-    const int t_fast = (B % kTileKeys == 0 && !slot_mode) ? max(0, nfull - (NS - 2)) : 0;
+    const int t_fast = (B % kTileKeys == 0 && !slot_mode) ? max(0, nfull - (SPLIT ? NS - 1 : NS - 2)) : 0;
     uint64_t fk = 0, fv = 0;     // K and V base of the next streamed tile (head h0)
+    uint64_t fv_prev = 0;        // SPLIT: V base of the tile before it (V runs one tile behind K)
     int f_left = 0, f_pidx = 0;  // tiles left in its page; the page's index in `pages`
     int32_t f_next = 0;          // page number at f_pidx + 1
     const uint32_t k_tile_b = kTileKeys * k_key_b, v_tile_b = kTileKeys * v_key_b;
@@ -836,12 +862,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
         }
     };
     auto fast_issue_v = [&](auto nt, int stage, int j) {
+        const void* base = reinterpret_cast<const void*>(SPLIT ? fv_prev : fv);
         if constexpr (decltype(nt)::value) {
-            dma_b128_s_nt(v_lane_h[j], reinterpret_cast<const void*>(fv),
-                          tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
+            dma_b128_s_nt(v_lane_h[j], base, tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
         } else {
-            dma_b128_s(v_lane_h[j], reinterpret_cast<const void*>(fv),
-                       tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
+            dma_b128_s(v_lane_h[j], base, tile_dst(V_REGION + stage * TILE_SET + j * HD::kTile));
         }
     };
     // D = 256: part P of this wave's streamed K (or V) keys.
@@ -857,12 +882,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     };
     auto fast_issue_v_part = [&](auto nt, auto part, int stage) {
         constexpr int P = decltype(part)::value;
+        const void* base = reinterpret_cast<const void*>(SPLIT ? fv_prev : fv);
         if constexpr (decltype(nt)::value) {
-            dma_b128_s_nt_o<128 * P>(v_lane_h[0], reinterpret_cast<const void*>(fv),
-                                     tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
+            dma_b128_s_nt_o<128 * P>(v_lane_h[0], base, tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
         } else {
-            dma_b128_s_o<128 * P>(v_lane_h[0], reinterpret_cast<const void*>(fv),
-                                  tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
+            dma_b128_s_o<128 * P>(v_lane_h[0], base, tile_dst(V_REGION + stage * TILE_SET + P * HD::kPartBytes));
         }
     };
     // D = 64: this wave's one streamed load per head and tile, K or V.
@@ -886,7 +910,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             f_left = B / kTileKeys;
         }
     };
-    wait_vmcnt<(NS - 3) * LPT>();
+    // SPLIT: a streamed step stages V of the tile behind the walker and K of the walker's tile,
+    // then moves both on; the walker starts at tile NS-1 (the first streamed K).
+    auto fast_shift = [&]() {
+        fv_prev = fv;
+        fast_advance();
+    };
+    if (SPLIT && t_fast > 0) fast_shift();
+    wait_vmcnt<SPLIT ? (NS - 3) * LPT + LPTK : (NS - 3) * LPT>();   // tile 0 staged
     __syncthreads();
     f32x16 s = f32x16{};
     V8 pb_prev[2], pl_prev[2];
@@ -932,29 +963,31 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 for (int b = 0; b < NS; ++b) {
                     const int t = t0 + b;
                     if (t >= t_fast) break;
-                    wait_vmcnt<(NS - 4) * LPT>();
+                    wait_vmcnt<WAIT_STEP>();
                     __syncthreads();
                     const int ds = (b + NS - 2) % NS;
+                    const int dks = SPLIT ? (b + NS - 1) % NS : ds;   // stage of the streamed K
                     auto piece = [&](int sl) {
                         if constexpr (D == 256) {
-                            if (sl == 2) fast_issue_k_part(nt, IntTag<0>{}, ds);
-                            if (sl == 4) fast_issue_k_part(nt, IntTag<1>{}, ds);
-                            if (sl == 6) fast_issue_k_part(nt, IntTag<2>{}, ds);
-                            if (sl == 8) fast_issue_k_part(nt, IntTag<3>{}, ds);
-                            if (sl == 10) fast_issue_v_part(nt, IntTag<0>{}, ds);
-                            if (sl == 12) fast_issue_v_part(nt, IntTag<1>{}, ds);
-                            if (sl == 14) fast_issue_v_part(nt, IntTag<2>{}, ds);
-                            if (sl == 18) fast_issue_v_part(nt, IntTag<3>{}, ds);
-                            if (sl == 24) fast_advance();
+                            if (sl == 2) fast_issue_v_part(nt, IntTag<0>{}, ds);
+                            if (sl == 4) fast_issue_v_part(nt, IntTag<1>{}, ds);
+                            if (sl == 6) fast_issue_v_part(nt, IntTag<2>{}, ds);
+                            if (sl == 8) fast_issue_v_part(nt, IntTag<3>{}, ds);
+                            if (sl == 10) fast_issue_k_part(nt, IntTag<0>{}, dks);
+                            if (sl == 12) fast_issue_k_part(nt, IntTag<1>{}, dks);
+                            if (sl == 14) fast_issue_k_part(nt, IntTag<2>{}, dks);
+                            if (sl == 18) fast_issue_k_part(nt, IntTag<3>{}, dks);
+                            if (sl == 24) fast_shift();
                         } else if constexpr (D == 128) {
                             if (HPW == 1) {
                                 if (sl == 4) fast_issue_k(nt, ds, 0);
                                 if (sl == 8) fast_issue_v(nt, ds, 0);
+                                if (sl == 12) fast_advance();
                             } else {
-                                if (sl == 3 || sl == 5) fast_issue_k(nt, ds, (sl - 3) >> 1);
-                                if (sl == 7 || sl == 9) fast_issue_v(nt, ds, (sl - 7) >> 1);
+                                if (sl == 3 || sl == 5) fast_issue_v(nt, ds, (sl - 3) >> 1);
+                                if (sl == 7 || sl == 9) fast_issue_k(nt, dks, (sl - 7) >> 1);
+                                if (sl == 12) fast_shift();
                             }
-                            if (sl == 12) fast_advance();
                         } else {
                             if (sl == 2 || (HPW == 2 && sl == 4)) fast_issue_kv(nt, ds, (sl - 2) >> 1);
                             if (sl == 6) fast_advance();
@@ -986,28 +1019,29 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 for (int b = 0; b < NS; ++b) {
                     const int t = t0 + b;
                     if (t >= t_fast) break;
-                    wait_vmcnt<(NS - 4) * LPT>();
+                    wait_vmcnt<WAIT_STEP>();
                     __syncthreads();
                     const int ds = (b + NS - 2) % NS;
+                    const int dks = SPLIT ? (b + NS - 1) % NS : ds;
                     if constexpr (D == 256) {
-                        fast_issue_k_part(nt, IntTag<0>{}, ds);
-                        fast_issue_k_part(nt, IntTag<1>{}, ds);
-                        fast_issue_k_part(nt, IntTag<2>{}, ds);
-                        fast_issue_k_part(nt, IntTag<3>{}, ds);
                         fast_issue_v_part(nt, IntTag<0>{}, ds);
                         fast_issue_v_part(nt, IntTag<1>{}, ds);
                         fast_issue_v_part(nt, IntTag<2>{}, ds);
                         fast_issue_v_part(nt, IntTag<3>{}, ds);
+                        fast_issue_k_part(nt, IntTag<0>{}, dks);
+                        fast_issue_k_part(nt, IntTag<1>{}, dks);
+                        fast_issue_k_part(nt, IntTag<2>{}, dks);
+                        fast_issue_k_part(nt, IntTag<3>{}, dks);
                     } else if constexpr (D == 128) {
 #pragma unroll
-                        for (int j = 0; j < HPW; ++j) fast_issue_k(nt, ds, j);
+                        for (int j = 0; j < HPW; ++j) fast_issue_k(nt, dks, j);
 #pragma unroll
                         for (int j = 0; j < HPW; ++j) fast_issue_v(nt, ds, j);
                     } else {
 #pragma unroll
                         for (int j = 0; j < HPW; ++j) fast_issue_kv(nt, ds, j);
                     }
-                    fast_advance();
+                    if constexpr (SPLIT) fast_shift(); else fast_advance();
                 }
             }
         }
@@ -1019,42 +1053,52 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     } else {
         fast_steps(NtTag<false>{});
     }
-    // The remaining steps: masks, partial and tree tiles, general DMA.
-    int pf = fetch(t_fast + NS - 2);
+    // The remaining steps: masks, partial and tree tiles, general DMA.  SPLIT: the first
+    // step stages V of tile t_fast + NS - 2 (its K is staged), so that tile is described here.
+    if constexpr (SPLIT) describe(t_fast + NS - 2, fetch(t_fast + NS - 2));
+    int pf = fetch(t_fast + (SPLIT ? NS - 1 : NS - 2));
     for (int t0 = t_fast - t_fast % NS; t0 < nt; t0 += NS) {
 #pragma unroll
         for (int b = 0; b < NS; ++b) {
             const int t = t0 + b;
             if (t < t_fast) continue;
             if (t >= nt) break;
-            wait_vmcnt<(NS - 4) * LPT>();
+            wait_vmcnt<WAIT_STEP>();
             __syncthreads();
-            // DMA of tile t+NS-2 into the retired stage, spread over the step's slots.
+            // DMA of tile t+NS-2 into the retired stage, spread over the step's slots.  SPLIT:
+            // V and ancestor words of tile t+NS-2 (described in the previous step) into the
+            // stage retired by P.V of tile t-2, then K of tile t+NS-1 into the stage of tile t-1.
             const int ds = (b + NS - 2) % NS;
+            const int dks = (b + NS - 1) % NS;
             auto piece = [&](int sl) {
-                if (sl == 1) describe(t + NS - 2, pf);
                 if constexpr (D == 256) {
-                    if (sl == 3) issue_k_part(IntTag<0>{}, ds);
-                    if (sl == 5) issue_k_part(IntTag<1>{}, ds);
-                    if (sl == 7) issue_k_part(IntTag<2>{}, ds);
-                    if (sl == 9) issue_k_part(IntTag<3>{}, ds);
-                    if (sl == 11) issue_v_part(IntTag<0>{}, ds);
-                    if (sl == 13) issue_v_part(IntTag<1>{}, ds);
-                    if (sl == 15) issue_v_part(IntTag<2>{}, ds);
-                    if (sl == 17) issue_v_part(IntTag<3>{}, ds);
-                    if (sl == 20) issue_mask(ds);
-                    if (sl == 22) pf = fetch(t + NS - 1);
+                    if (sl == 1) issue_v_part(IntTag<0>{}, ds);
+                    if (sl == 3) issue_v_part(IntTag<1>{}, ds);
+                    if (sl == 5) issue_v_part(IntTag<2>{}, ds);
+                    if (sl == 7) issue_v_part(IntTag<3>{}, ds);
+                    if (sl == 8) issue_mask(ds);
+                    if (sl == 9) describe(t + NS - 1, pf);
+                    if (sl == 11) issue_k_part(IntTag<0>{}, dks);
+                    if (sl == 13) issue_k_part(IntTag<1>{}, dks);
+                    if (sl == 15) issue_k_part(IntTag<2>{}, dks);
+                    if (sl == 17) issue_k_part(IntTag<3>{}, dks);
+                    if (sl == 22) pf = fetch(t + NS);
                 } else if constexpr (D == 128) {
                     if (HPW == 1) {
+                        if (sl == 1) describe(t + NS - 2, pf);
                         if (sl == 4) issue_k(ds, 0);
                         if (sl == 8) issue_v(ds, 0);
+                        if (sl == 12) issue_mask(ds);
+                        if (sl == 13) pf = fetch(t + NS - 1);
                     } else {
-                        if (sl == 3 || sl == 5) issue_k(ds, (sl - 3) >> 1);
-                        if (sl == 7 || sl == 9) issue_v(ds, (sl - 7) >> 1);
+                        if (sl == 1 || sl == 3) issue_v(ds, (sl - 1) >> 1);
+                        if (sl == 4) issue_mask(ds);
+                        if (sl == 5) describe(t + NS - 1, pf);
+                        if (sl == 7 || sl == 9) issue_k(dks, (sl - 7) >> 1);
+                        if (sl == 13) pf = fetch(t + NS);
                     }
-                    if (sl == 12) issue_mask(ds);
-                    if (sl == 13) pf = fetch(t + NS - 1);
                 } else {
+                    if (sl == 1) describe(t + NS - 2, pf);
                     if (sl == 2 || (HPW == 2 && sl == 4)) issue_kv(ds, (sl - 2) >> 1);
                     if (sl == 5) issue_mask(ds);
                     if (sl == 6) pf = fetch(t + NS - 1);
