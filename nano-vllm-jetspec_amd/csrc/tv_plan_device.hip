@@ -62,30 +62,40 @@ __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) { return (x + 
 __device__ __forceinline__ int64_t cost_weight(int hpw) { return hpw == 2 ? 5 : 4; }
 
 constexpr int kPlanWaves = kPlanThreads / 64;
+constexpr int kProbeWaves = 4;   // waves that probe chunk targets in the refit (one per SIMD)
 
-// Block-wide exclusive scan of one int per thread (kPlanThreads threads); returns the
-// thread's prefix and writes the total to *total.  A scan within each wave (lane
-// shuffles), then the wave totals through LDS: two barriers.
-__device__ int64_t block_scan(int64_t v, int64_t* scratch, int64_t* total) {
+// Block-wide exclusive scan of three int64 values per thread (kPlanThreads threads): each
+// thread's prefixes of v[0..2] are returned in v, the totals written to total[0..2].  A scan
+// within each wave (lane shuffles), then the wave totals through LDS: two barriers.
+__device__ void block_scan3(int64_t (&v)[3], int64_t* scratch, int64_t* total) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    int64_t x = v;
+    int64_t x[3] = {v[0], v[1], v[2]};
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        const int64_t y = __shfl_up(x, off);
-        if (lane >= off) x += y;
-    }
-    if (lane == 63) scratch[w] = x;
-    __syncthreads();
-    int64_t before = 0, all = 0;
 #pragma unroll
-    for (int k = 0; k < kPlanWaves; ++k) {
-        const int64_t s = scratch[k];
-        before += k < w ? s : 0;
-        all += s;
+        for (int j = 0; j < 3; ++j) {
+            const int64_t y = __shfl_up(x[j], off);
+            if (lane >= off) x[j] += y;
+        }
     }
-    if (t == 0) *total = all;
-    __syncthreads();   // *total is visible, and every thread has read `scratch`
-    return before + x - v;
+    if (lane == 63) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) scratch[3 * w + j] = x[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        int64_t before = 0, all = 0;
+#pragma unroll
+        for (int k = 0; k < kPlanWaves; ++k) {
+            const int64_t s = scratch[3 * k + j];
+            before += k < w ? s : 0;
+            all += s;
+        }
+        if (t == 0) total[j] = all;
+        v[j] = before + x[j] - v[j];
+    }
+    __syncthreads();   // the totals are visible, and every thread has read `scratch`
 }
 
 // Sum over one wave (returned to every lane).
@@ -97,81 +107,99 @@ __device__ __forceinline__ int64_t wave_sum(int64_t v) {
 
 // Block-wide sum of one int64 per thread (kPlanThreads threads), returned to all.
 __device__ int64_t block_sum(int64_t v, int64_t* scratch) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    v = wave_sum(v);
     const int t = threadIdx.x;
     __syncthreads();
     if ((t & 63) == 0) scratch[t >> 6] = v;
     __syncthreads();
     int64_t total = 0;
-    for (int w = 0; w < kPlanThreads / 64; ++w) total += scratch[w];
+#pragma unroll
+    for (int w = 0; w < kPlanWaves; ++w) total += scratch[w];
     __syncthreads();   // every thread has read `scratch` before anyone reuses it
     return total;
 }
 
-// The host planner's chunk length for a prefix of p keys and chunk target tau.
-__device__ __forceinline__ int64_t chunk_for(int64_t p, int hpw, int64_t tau, int64_t max_chunk) {
-    int64_t chunk = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), tau / cost_weight(hpw)), 32), max_chunk);
-    const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
-    chunk = round_up((p + nchunks - 1) / max<int64_t>(nchunks, 1), 32);
+// One request's geometry from its (clamped) node count: KV heads per item, nodes per item,
+// head groups and node blocks (heads_per_group and nodes_per_item with nw = 32 / qpk nodes
+// per wave taken once per thread, so only the node-block count divides).
+struct ReqShape {
+    int hpw, npw, G, NB;
+};
+__device__ __forceinline__ ReqShape req_shape(int n, int kv_heads, int nw) {
+    ReqShape s;
+    s.hpw = (n <= 4 * nw && kv_heads >= 2) ? 2 : 1;
+    s.npw = (8 / s.hpw) * nw;
+    s.G = s.hpw == 2 ? (kv_heads + 1) >> 1 : kv_heads;
+    s.NB = (n + s.npw - 1) / s.npw;
+    return s;
+}
+
+// The host planner's chunk length (tv_plan.cpp, chunk_for) for a prefix of p keys, with
+// q = tau / cost_weight(hpw) precomputed: min(round_up(max(64, q), 32), max_chunk), then
+// equalised over the chunks.  Every quantity after the first min is below 2^32.
+__device__ __forceinline__ uint32_t chunk_of(uint32_t p, int64_t q, int64_t max_chunk) {
+    const int64_t c0 = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), min(q, max_chunk)), 32), max_chunk);
+    const uint32_t c = static_cast<uint32_t>(c0);
+    const uint32_t nchunks = p > 0 ? (p + c - 1) / c : 1;
+    const uint32_t chunk = ((p + nchunks - 1) / nchunks + 31) / 32 * 32;
     return chunk < 32 ? 32 : chunk;
 }
 
+// Plans in one 1024-thread workgroup.  The prefix lengths and node counts are read once into
+// LDS; every later per-request quantity comes from there.
 __global__ void __launch_bounds__(kPlanThreads)
 plan_device_kernel(const PlanArgs a) {
     __shared__ uint64_t keys[kMaxSortItems];
-    __shared__ int64_t scan[kPlanThreads];
-    __shared__ int64_t totals[4];
+    __shared__ int32_t stream_id[kMaxSortItems];   // (request, head group, chunk) of each sorted item
+    __shared__ int32_t req_p[kMaxPlanRequests], req_n[kMaxPlanRequests];
     __shared__ int32_t req_chunk[kMaxPlanRequests], req_nchunks[kMaxPlanRequests];
     __shared__ int32_t req_item_off[kMaxPlanRequests], req_group_off[kMaxPlanRequests], req_slot_off[kMaxPlanRequests];
-    __shared__ int32_t stream_id[kMaxSortItems];   // (request, head group, chunk) of each sorted item
+    __shared__ int64_t scan[3 * kPlanWaves];
+    __shared__ int64_t totals[4];
     __shared__ int shared_flag;
     __shared__ int32_t probe_fits[kPlanWaves];
+    __shared__ int64_t probe_val[kPlanWaves];
     const int t = threadIdx.x;
     const int R = a.num_requests;
     const int B = a.block_size;
+    const int KV = a.num_kv_heads, QPK = a.qpk, NW = 32 / a.qpk;
 
-    // 1. Costs and their total.
-    int64_t my_cost = 0;
+    // 1. Prefix lengths and node counts into LDS (clamped; a value outside the planner's
+    // range fails the plan), costs and their total.
+    if (t == 0) shared_flag = 0;
     bool bad = false;
+    int64_t my_cost = 0;
     for (int r = t; r < R; r += kPlanThreads) {
         const int p = a.prefix_lens[r], n = a.node_counts[r];
-        if (p < 0 || n < 1 || n > 1024) {
-            bad = true;
-            continue;
-        }
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int npw = nodes_per_item(hpw, a.qpk);
-        const int64_t groups = (a.num_kv_heads + hpw - 1) / hpw;
-        const int64_t blocks = (n + npw - 1) / npw;
-        my_cost += groups * blocks * cost_weight(hpw) * (static_cast<int64_t>(p) + n);
+        bad |= p < 0 || n < 1 || n > 1024;
+        const int pc = max(0, p), nc = max(1, min(1024, n));
+        req_p[r] = pc;
+        req_n[r] = nc;
+        const ReqShape s = req_shape(nc, KV, NW);
+        my_cost += static_cast<int64_t>(s.G) * s.NB * cost_weight(s.hpw) * (static_cast<int64_t>(pc) + nc);
     }
-    if (t == 0) shared_flag = 0;
-    __syncthreads();
+    __syncthreads();   // shared_flag is cleared before anyone sets it
     if (bad) atomicOr(&shared_flag, 1);
-    const int64_t cost_before = block_scan(my_cost, scan, &totals[0]);
-    (void)cost_before;
-    const int64_t total_cost = totals[0];
+    const int64_t total_cost = block_sum(my_cost, scan);   // its barriers also publish req_p / req_n
     const int64_t target = max(static_cast<int64_t>(kMinChunkKeys), total_cost / a.compute_units);
-    const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * B) / 32 * 32;
+    const int64_t max_chunk = min((static_cast<int64_t>(kMaxChunkPages - 1) * B) / 32 * 32, int64_t{1} << 31);
 
     // 1b. The host's refit of the chunk target when the items leave the last of at most
     // kFillRounds rounds part-empty: the smallest target whose item count fits the same
     // rounds.  The count falls as the target grows, so any search finds the host's
-    // bisection result; here each of the 16 waves probes one target per round (a
-    // 17-way search, one barrier per round).
-    auto request_items = [&](int r, int64_t tau) -> int64_t {
-        const int64_t p = max(0, a.prefix_lens[r]);
-        const int nodes = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(nodes, a.num_kv_heads, a.qpk);
-        const int npw = nodes_per_item(hpw, a.qpk);
-        const int64_t units = static_cast<int64_t>((a.num_kv_heads + hpw - 1) / hpw) * ((nodes + npw - 1) / npw);
-        const int64_t chunk = chunk_for(p, hpw, tau, max_chunk);
-        return units * (p > 0 ? (p + chunk - 1) / chunk : 1);
+    // bisection result; here one wave per SIMD probes one target per round (a 5-way
+    // search, two barriers per round; more probing waves would share the SIMDs and make
+    // every round as much longer).
+    auto request_items = [&](int r, int64_t q4, int64_t q5) -> int64_t {
+        const uint32_t p = static_cast<uint32_t>(req_p[r]);
+        const ReqShape s = req_shape(req_n[r], KV, NW);
+        const uint32_t chunk = chunk_of(p, s.hpw == 2 ? q5 : q4, max_chunk);
+        return static_cast<int64_t>(s.G) * s.NB * (p > 0 ? (p + chunk - 1) / chunk : 1u);
     };
     int64_t tau = target;
     if (a.chunk_keys == 0) {
         int64_t now = 0;
-        for (int r = t; r < R; r += kPlanThreads) now += request_items(r, target);
+        for (int r = t; r < R; r += kPlanThreads) now += request_items(r, target / 4, target / 5);
         now = block_sum(now, scan);
         const int64_t rounds = (now + a.compute_units - 1) / a.compute_units;
         if (now > a.compute_units && rounds <= kFillRounds) {
@@ -180,16 +208,22 @@ plan_device_kernel(const PlanArgs a) {
             int64_t lo = 1, hi = target;   // items(hi) <= limit; the answer is in [lo, hi]
             while (lo < hi) {
                 const int64_t span = hi - lo;
-                const int64_t probe = lo + span * (w + 1) / (kPlanWaves + 1);   // in [lo, hi)
-                int64_t n = 0;
-                for (int r = lane; r < R; r += 64) n += request_items(r, probe);
-                n = wave_sum(n);
-                if (lane == 0) probe_fits[w] = n <= limit ? 1 : 0;
+                if (w < kProbeWaves) {
+                    const int64_t probe = lo + span * (w + 1) / (kProbeWaves + 1);   // in [lo, hi)
+                    const int64_t q4 = probe / 4, q5 = probe / 5;
+                    int64_t n = 0;
+                    for (int r = lane; r < R; r += 64) n += request_items(r, q4, q5);
+                    n = wave_sum(n);
+                    if (lane == 0) {
+                        probe_fits[w] = n <= limit ? 1 : 0;
+                        probe_val[w] = probe;
+                    }
+                }
                 __syncthreads();
                 int64_t new_lo = lo, new_hi = hi;
 #pragma unroll
-                for (int k = 0; k < kPlanWaves; ++k) {
-                    const int64_t pk = lo + span * (k + 1) / (kPlanWaves + 1);
+                for (int k = 0; k < kProbeWaves; ++k) {
+                    const int64_t pk = probe_val[k];
                     if (probe_fits[k]) new_hi = min(new_hi, pk); else new_lo = max(new_lo, pk + 1);
                 }
                 __syncthreads();   // every thread has read probe_fits
@@ -204,39 +238,37 @@ plan_device_kernel(const PlanArgs a) {
     // thread so that one scan yields request-ordered offsets.
     const int per_thread = (R + kPlanThreads - 1) / kPlanThreads;
     const int r0 = min(R, t * per_thread), r1 = min(R, r0 + per_thread);
-    int64_t my_items = 0, my_groups = 0, my_slots = 0;
-    for (int r = r0; r < r1; ++r) {
-        const int p = max(0, a.prefix_lens[r]);
-        const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int npw = nodes_per_item(hpw, a.qpk);
-        const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int64_t NB = (n + npw - 1) / npw;
-        const int64_t chunk = a.chunk_keys > 0 ? a.chunk_keys : chunk_for(p, hpw, tau, max_chunk);
-        const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
-        req_chunk[r] = static_cast<int32_t>(chunk);
-        req_nchunks[r] = static_cast<int32_t>(nchunks);
-        my_items += G * NB * nchunks;
-        if (nchunks > 1) {
-            my_groups += G * NB;
-            my_slots += G * NB * nchunks;
+    int64_t mine[3] = {0, 0, 0};   // items, groups, slots
+    {
+        const int64_t q4 = tau / 4, q5 = tau / 5;
+        for (int r = r0; r < r1; ++r) {
+            const uint32_t p = static_cast<uint32_t>(req_p[r]);
+            const ReqShape s = req_shape(req_n[r], KV, NW);
+            const uint32_t chunk = a.chunk_keys > 0 ? static_cast<uint32_t>(a.chunk_keys)
+                                                    : chunk_of(p, s.hpw == 2 ? q5 : q4, max_chunk);
+            const uint32_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1u;
+            req_chunk[r] = static_cast<int32_t>(chunk);
+            req_nchunks[r] = static_cast<int32_t>(nchunks);
+            const int64_t units = static_cast<int64_t>(s.G) * s.NB;
+            mine[0] += units * nchunks;
+            if (nchunks > 1) {
+                mine[1] += units;
+                mine[2] += units * nchunks;
+            }
         }
     }
-    int64_t item_base = block_scan(my_items, scan, &totals[1]);
-    int64_t group_base = block_scan(my_groups, scan, &totals[2]);
-    int64_t slot_base = block_scan(my_slots, scan, &totals[3]);
+    int64_t base[3] = {mine[0], mine[1], mine[2]};
+    block_scan3(base, scan, &totals[1]);
     for (int r = r0; r < r1; ++r) {
-        const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int64_t G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int64_t NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
-        req_item_off[r] = static_cast<int32_t>(item_base);
-        req_group_off[r] = static_cast<int32_t>(group_base);
-        req_slot_off[r] = static_cast<int32_t>(slot_base);
-        item_base += G * NB * req_nchunks[r];
-        if (req_nchunks[r] > 1) {
-            group_base += G * NB;
-            slot_base += G * NB * req_nchunks[r];
+        const ReqShape s = req_shape(req_n[r], KV, NW);
+        const int64_t units = static_cast<int64_t>(s.G) * s.NB, nc = req_nchunks[r];
+        req_item_off[r] = static_cast<int32_t>(base[0]);
+        req_group_off[r] = static_cast<int32_t>(base[1]);
+        req_slot_off[r] = static_cast<int32_t>(base[2]);
+        base[0] += units * nc;
+        if (nc > 1) {
+            base[1] += units;
+            base[2] += units * nc;
         }
     }
     __syncthreads();
@@ -252,219 +284,244 @@ plan_device_kernel(const PlanArgs a) {
         }
         return;
     }
+    const int nitems = static_cast<int>(num_items);
 
-    // 3. Sort keys: (~cost, request, head group, chunk, block), each item's secondary
-    // index being its rank in that (request, head group, chunk, block) enumeration.
-    int npow = 1;
-    while (npow < num_items) npow <<= 1;
-    for (int e = t; e < npow; e += kPlanThreads) keys[e] = ~0ull;
-    __syncthreads();
-    for (int r = r0; r < r1; ++r) {
-        const int p = max(0, a.prefix_lens[r]);
-        const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
-        const int nc = req_nchunks[r];
-        const int64_t chunk = req_chunk[r];
-        for (int hg = 0; hg < G; ++hg) {
-            for (int c = 0; c < nc; ++c) {
-                const int64_t kb = min(static_cast<int64_t>(p), c * chunk), ke = min(static_cast<int64_t>(p), (c + 1) * chunk);
-                const int64_t cost = cost_weight(hpw) * ((ke - kb) + (c == nc - 1 ? n : 0));
-                for (int nb = 0; nb < NB; ++nb) {
-                    const int64_t idx = req_item_off[r] + (static_cast<int64_t>(hg) * nc + c) * NB + nb;
-                    keys[idx] = (static_cast<uint64_t>(0x7fffffffu - static_cast<uint32_t>(cost)) << 32) |
-                                static_cast<uint32_t>(idx);
-                }
-            }
-        }
-    }
-    __syncthreads();
-    for (int size = 2; size <= npow; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int e = t; e < npow; e += kPlanThreads) {
-                const int partner = e ^ stride;
-                if (partner > e) {
-                    const bool ascending = (e & size) == 0;
-                    const uint64_t x = keys[e], y = keys[partner];
-                    if ((x > y) == ascending) {
-                        keys[e] = y;
-                        keys[partner] = x;
-                    }
-                }
-            }
-            // A stride below 64 pairs elements that one wave owns (e and e ^ stride differ
-            // only in bits below 64, and thread t owns e = t + k * kPlanThreads).  Between
-            // two such stages the wave's own LDS ordering is enough; a workgroup barrier
-            // precedes and follows every stage whose pairs cross waves, and the last stage.
-            const int next_stride = stride > 1 ? stride >> 1 : size;
-            if (stride < 64 && next_stride < 64 && size < npow) {
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            } else {
-                __syncthreads();
-            }
-        }
-    }
-
-    // Decode a sorted key back into its item (request found by the offsets).
-    auto decode = [&](int64_t sorted_pos, int32_t* out) {
-        const int64_t idx = static_cast<int64_t>(keys[sorted_pos] & 0xffffffffull);
-        int lo = 0, hi = R - 1;
-        while (lo < hi) {      // last request whose item offset is <= idx
-            const int mid = (lo + hi + 1) >> 1;
-            if (req_item_off[mid] <= idx) lo = mid; else hi = mid - 1;
-        }
-        const int r = lo;
-        const int p = max(0, a.prefix_lens[r]);
-        const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
-        const int nc = req_nchunks[r];
-        const int64_t local = idx - req_item_off[r];
-        const int nb = static_cast<int>(local % NB);
-        const int64_t hc = local / NB;
-        const int c = static_cast<int>(hc % nc);
-        const int hg = static_cast<int>(hc / nc);
-        const int64_t chunk = req_chunk[r];
-        out[0] = r;
-        out[1] = hg * hpw;
-        out[2] = nb * nodes_per_item(hpw, a.qpk);
-        out[3] = static_cast<int32_t>(min(static_cast<int64_t>(p), c * chunk));
-        out[4] = static_cast<int32_t>(min(static_cast<int64_t>(p), (c + 1) * chunk));
-        out[5] = (c == nc - 1 ? kItemLastChunk : 0) | (nb == NB - 1 ? kItemLastBlock : 0) | (a.qpk << kItemGroupShift);
-        out[6] = nc > 1 ? req_slot_off[r] + (hg * NB + nb) * nc + c : -1;
-        out[7] = hpw;
-    };
-    // Stream identity (request, head group, chunk) of a sorted position.
-    auto stream_of = [&](int64_t sorted_pos) -> int64_t {
-        const int64_t idx = static_cast<int64_t>(keys[sorted_pos] & 0xffffffffull);
+    // The request of item enumeration index idx (the last request whose first item is at or
+    // before it; every request has at least one item).
+    auto request_of = [&](int idx) -> int {
         int lo = 0, hi = R - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (req_item_off[mid] <= idx) lo = mid; else hi = mid - 1;
         }
-        const int n = max(1, min(1024, a.node_counts[lo]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
-        return (static_cast<int64_t>(lo) << 32) | ((idx - req_item_off[lo]) / NB);
+        return lo;
     };
 
-    // 4. XCD placement (tv_plan.cpp::place_for_xcds) and output.
-    for (int64_t i = t; i < num_items; i += kPlanThreads) {
-        const int64_t s = stream_of(i);
-        stream_id[i] = static_cast<int32_t>((s >> 32) * kMaxSortItems + (s & 0xffffffff));
+    // 3. Sort keys, one thread per item: (~cost, request, head group, chunk, block), the
+    // enumeration index idx = item offset + (hg * nchunks + c) * NB + nb being the tie order.
+    int npow = 1;
+    while (npow < nitems) npow <<= 1;
+    for (int e = t; e < npow; e += kPlanThreads) {
+        uint64_t key = ~0ull;
+        if (e < nitems) {
+            const int r = request_of(e);
+            const ReqShape s = req_shape(req_n[r], KV, NW);
+            const int nc = req_nchunks[r];
+            const int local = e - req_item_off[r];
+            const int c = (local / s.NB) % nc;
+            const int64_t p = req_p[r], chunk = req_chunk[r];
+            const int64_t kb = min(p, c * chunk), ke = min(p, (c + 1) * chunk);
+            const int64_t cost = cost_weight(s.hpw) * ((ke - kb) + (c == nc - 1 ? req_n[r] : 0));
+            key = (static_cast<uint64_t>(0x7fffffffu - static_cast<uint32_t>(cost)) << 32) | static_cast<uint32_t>(e);
+        }
+        keys[e] = key;
+    }
+    __syncthreads();
+    // Bitonic sort of npow keys, longest first.  Thread t owns elements t + k * kPlanThreads;
+    // a stride below 64 pairs two elements of one wave with the same k, so those stages run
+    // on registers with lane shuffles (the keys are loaded once per run of such stages, and
+    // waves that own no element skip them), and the stages of larger strides exchange
+    // through LDS with a barrier each.  `in_regs` depends only on the loop position, so every
+    // wave takes the same barriers.
+    constexpr int kPer = kMaxSortItems / kPlanThreads;
+    const bool owns = t - (t & 63) < npow;   // wave-uniform
+    uint64_t x[kPer];
+    bool in_regs = false;
+    for (int size = 2; size <= npow; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            if (stride >= 64) {
+                if (in_regs) {
+                    if (owns) {
+#pragma unroll
+                        for (int k = 0; k < kPer; ++k) {
+                            const int e = t + k * kPlanThreads;
+                            if (e < npow) keys[e] = x[k];
+                        }
+                    }
+                    __syncthreads();
+                    in_regs = false;
+                }
+                for (int e = t; e < npow; e += kPlanThreads) {
+                    const int partner = e ^ stride;
+                    if (partner > e) {
+                        const bool ascending = (e & size) == 0;
+                        const uint64_t u = keys[e], v = keys[partner];
+                        if ((u > v) == ascending) {
+                            keys[e] = v;
+                            keys[partner] = u;
+                        }
+                    }
+                }
+                __syncthreads();
+                continue;
+            }
+            if (!in_regs) {
+                if (owns) {
+#pragma unroll
+                    for (int k = 0; k < kPer; ++k) {
+                        const int e = t + k * kPlanThreads;
+                        x[k] = e < npow ? keys[e] : ~0ull;
+                    }
+                }
+                in_regs = true;
+            }
+            if (owns) {
+                const bool lower = (t & stride) == 0;
+#pragma unroll
+                for (int k = 0; k < kPer; ++k) {
+                    const int e = t + k * kPlanThreads;
+                    if (k * kPlanThreads < npow) {   // wave-uniform: the wave's elements of row k exist
+                        const uint32_t lo32 = __shfl_xor(static_cast<uint32_t>(x[k]), stride);
+                        const uint32_t hi32 = __shfl_xor(static_cast<uint32_t>(x[k] >> 32), stride);
+                        const uint64_t y = (static_cast<uint64_t>(hi32) << 32) | lo32;
+                        const bool ascending = (e & size) == 0;
+                        x[k] = (lower == ascending) ? min(x[k], y) : max(x[k], y);
+                    }
+                }
+            }
+        }
+    }
+    if (in_regs && owns) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int e = t + k * kPlanThreads;
+            if (e < npow) keys[e] = x[k];
+        }
+    }
+    __syncthreads();
+
+    // Decode a sorted key back into its item.
+    auto decode = [&](int sorted_pos, int32_t* out) {
+        const int idx = static_cast<int>(keys[sorted_pos] & 0xffffffffull);
+        const int r = request_of(idx);
+        const ReqShape s = req_shape(req_n[r], KV, NW);
+        const int nc = req_nchunks[r];
+        const int local = idx - req_item_off[r];
+        const int nb = local % s.NB;
+        const int hc = local / s.NB;
+        const int c = hc % nc;
+        const int hg = hc / nc;
+        const int64_t p = req_p[r], chunk = req_chunk[r];
+        out[0] = r;
+        out[1] = hg * s.hpw;
+        out[2] = nb * s.npw;
+        out[3] = static_cast<int32_t>(min(p, c * chunk));
+        out[4] = static_cast<int32_t>(min(p, (c + 1) * chunk));
+        out[5] = (c == nc - 1 ? kItemLastChunk : 0) | (nb == s.NB - 1 ? kItemLastBlock : 0) | (QPK << kItemGroupShift);
+        out[6] = nc > 1 ? req_slot_off[r] + (hg * s.NB + nb) * nc + c : -1;
+        out[7] = s.hpw;
+    };
+
+    // 4. XCD placement (tv_plan.cpp::place_for_xcds) and output.  Stream identity (request,
+    // head group, chunk) of each sorted position.
+    for (int i = t; i < nitems; i += kPlanThreads) {
+        const int idx = static_cast<int>(keys[i] & 0xffffffffull);
+        const int r = request_of(idx);
+        const ReqShape s = req_shape(req_n[r], KV, NW);
+        stream_id[i] = r * kMaxSortItems + (idx - req_item_off[r]) / s.NB;
     }
     if (t == 0) shared_flag = 0;
     __syncthreads();
     // Bit 0: some stream has several items; bit 1: some stream's item count (its
     // request's node blocks) is not a multiple of 8.
-    for (int64_t i = 1 + t; i < num_items; i += kPlanThreads) {
+    for (int i = 1 + t; i < nitems; i += kPlanThreads) {
         if (stream_id[i] == stream_id[i - 1]) atomicOr(&shared_flag, 1);
     }
     for (int r = t; r < R; r += kPlanThreads) {
-        const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
-        if (NB > 1 && NB % kXcds) atomicOr(&shared_flag, 2);
+        const ReqShape s = req_shape(req_n[r], KV, NW);
+        if (s.NB > 1 && s.NB % kXcds) atomicOr(&shared_flag, 2);
     }
     __syncthreads();
     const bool shared = (shared_flag & 1) != 0;
     const bool aligned = (shared_flag & 2) == 0;
     constexpr int kWindow = kXcds * kXcds;
-    const int64_t full = shared ? (num_items / kWindow) * kWindow : 0;
-    auto position_of = [&](int64_t rank) {
+    const int full = shared ? (nitems / kWindow) * kWindow : 0;
+    auto position_of = [&](int rank) {
         if (rank >= full) return rank;
-        const int64_t w = rank - rank % kWindow;
-        const int k = static_cast<int>(rank - w);
+        const int w = rank - rank % kWindow;
+        const int k = rank - w;
         const int column = (w / kWindow) % 2 ? kXcds - 1 - k / kXcds : k / kXcds;   // odd windows mirrored
         return w + kXcds * (k % kXcds) + column;
     };
     if (shared && aligned) {
         // Groups ahead of the at most 7 singles before them since the last multiple of
         // 8: ranks from the number of single items before each sorted position.
-        constexpr int kPer = kMaxSortItems / kPlanThreads;
-        const int64_t i0 = static_cast<int64_t>(t) * kPer;
+        const int i0 = t * kPer;
         uint32_t single_bits = 0;
-        int64_t mine = 0;
+        int64_t counted[3] = {0, 0, 0};
         for (int e = 0; e < kPer; ++e) {
-            const int64_t i = i0 + e;
-            if (i >= num_items) break;
+            const int i = i0 + e;
+            if (i >= nitems) break;
             const int32_t sid = stream_id[i];
-            const bool single = !((i > 0 && stream_id[i - 1] == sid) || (i + 1 < num_items && stream_id[i + 1] == sid));
+            const bool single = !((i > 0 && stream_id[i - 1] == sid) || (i + 1 < nitems && stream_id[i + 1] == sid));
             single_bits |= static_cast<uint32_t>(single) << e;
-            mine += single;
+            counted[0] += single;
         }
-        const int64_t before = block_scan(mine, scan, &totals[0]);   // syncs: stream_id reads are done
-        const int64_t singles_total = totals[0];
-        int64_t run = before;
+        block_scan3(counted, scan, &totals[0]);   // syncs: stream_id reads are done
+        const int singles_total = static_cast<int>(totals[0]);
+        int run = static_cast<int>(counted[0]);
         for (int e = 0; e < kPer; ++e) {
-            const int64_t i = i0 + e;
-            if (i >= num_items) break;
-            stream_id[i] = static_cast<int32_t>(run);                 // now: singles before position i
+            const int i = i0 + e;
+            if (i >= nitems) break;
+            stream_id[i] = run;                 // now: singles before position i
             run += (single_bits >> e) & 1u;
         }
         __syncthreads();
-        auto singles_before = [&](int64_t q) -> int64_t { return q < num_items ? stream_id[q] : singles_total; };
-        for (int e = 0; e < kPer; ++e) {
-            const int64_t i = i0 + e;
-            if (i >= num_items) break;
-            const int64_t sb = stream_id[i];
-            int64_t rank;
-            if (!((single_bits >> e) & 1u)) {
+        auto singles_before = [&](int q) -> int { return q < nitems ? stream_id[q] : singles_total; };
+        // Ranks and output, one item per thread (position i is single iff the count steps there).
+        for (int i = t; i < nitems; i += kPlanThreads) {
+            const int sb = stream_id[i];
+            int rank;
+            if (singles_before(i + 1) == sb) {
                 rank = (i - sb) + sb / kXcds * kXcds;
             } else {
-                int64_t lo = i + 1, hi = num_items;   // first q with floor8(singles before q) > sb
+                int lo = i + 1, hi = nitems;   // first q with floor8(singles before q) > sb
                 while (lo < hi) {
-                    const int64_t mid = (lo + hi) >> 1;
+                    const int mid = (lo + hi) >> 1;
                     if (singles_before(mid) / kXcds * kXcds > sb) hi = mid; else lo = mid + 1;
                 }
                 rank = sb + (lo - singles_before(lo));
             }
-            decode(i, a.items + position_of(rank) * 8);
+            decode(i, a.items + static_cast<int64_t>(position_of(rank)) * 8);
         }
     } else {
-        for (int64_t i = t; i < num_items; i += kPlanThreads) {
-            int64_t rank = i;
+        for (int i = t; i < nitems; i += kPlanThreads) {
+            int rank = i;
             if (i < full) {
-                const int64_t w = i - i % kWindow;
-                const int k = static_cast<int>(i - w);
+                const int w = i - i % kWindow;
+                const int k = i - w;
                 // Rank of item k in the window's "grouped first" order.
                 auto grouped = [&](int j) {
                     const int32_t s = stream_id[w + j];
                     return (j + 1 < kWindow && stream_id[w + j + 1] == s) || (j > 0 && stream_id[w + j - 1] == s);
                 };
-                const bool mine = grouped(k);
+                const bool mine_grouped = grouped(k);
                 int within = 0;
                 for (int j = 0; j < kWindow; ++j) {
                     if (j == k) continue;
                     const bool g = grouped(j);
-                    if (mine ? (g && j < k) : (g || j < k)) ++within;
+                    if (mine_grouped ? (g && j < k) : (g || j < k)) ++within;
                 }
                 rank = w + within;
             }
-            decode(i, a.items + position_of(rank) * 8);
+            decode(i, a.items + static_cast<int64_t>(position_of(rank)) * 8);
         }
     }
     // Merge groups in (request, head group, block) order with their first partial slot.
     for (int r = r0; r < r1; ++r) {
         const int nc = req_nchunks[r];
         if (nc < 2) continue;
-        const int n = max(1, min(1024, a.node_counts[r]));
-        const int hpw = heads_per_group(n, a.num_kv_heads, a.qpk);
-        const int G = (a.num_kv_heads + hpw - 1) / hpw;
-        const int NB = (n + nodes_per_item(hpw, a.qpk) - 1) / nodes_per_item(hpw, a.qpk);
-        for (int hg = 0; hg < G; ++hg) {
-            for (int nb = 0; nb < NB; ++nb) {
-                int32_t* gr = a.groups + static_cast<int64_t>(req_group_off[r] + hg * NB + nb) * 8;
+        const ReqShape s = req_shape(req_n[r], KV, NW);
+        for (int hg = 0; hg < s.G; ++hg) {
+            for (int nb = 0; nb < s.NB; ++nb) {
+                int32_t* gr = a.groups + static_cast<int64_t>(req_group_off[r] + hg * s.NB + nb) * 8;
                 gr[0] = r;
-                gr[1] = hg * hpw;
-                gr[2] = nb * nodes_per_item(hpw, a.qpk);
-                gr[3] = hpw;
-                gr[4] = req_slot_off[r] + (hg * NB + nb) * nc;
+                gr[1] = hg * s.hpw;
+                gr[2] = nb * s.npw;
+                gr[3] = s.hpw;
+                gr[4] = req_slot_off[r] + (hg * s.NB + nb) * nc;
                 gr[5] = nc;
-                gr[6] = a.qpk;   // the grouping the slots' rows are laid out for
+                gr[6] = QPK;   // the grouping the slots' rows are laid out for
                 gr[7] = 0;
             }
         }
