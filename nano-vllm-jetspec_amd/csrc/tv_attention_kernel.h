@@ -266,12 +266,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // at D = 256 each wave moves 8 keys of K and of V, one load per part.
     constexpr int LPT = D == 128 ? 2 * HPW : (D == 64 ? HPW : 2 * HD::kParts);
     static_assert(M_REGION + NS * kMaskBytes <= kRingBytes, "ring exceeds its LDS region");
-    // A 4-stage ring stages K one tile further ahead than V (SPLIT): in step t, K of tile t+3
-    // goes into the stage of tile t-1, whose K was last read in step t-2 (its V is still read
-    // in step t), and V (with the ancestor words) of tile t+2 into the stage of tile t-2.  K
-    // then has two steps to arrive and V three, and each step waits only for the loads issued
-    // two steps back: two tile sets in flight per workgroup instead of one.
-    constexpr bool SPLIT = NS == 4;
+    // At D = 256 the 4-stage ring stages K one tile further ahead than V (SPLIT): in step t, K
+    // of tile t+3 goes into the stage of tile t-1, whose K was last read in step t-2 (its V is
+    // still read in step t), and V (with the ancestor words) of tile t+2 into the stage of tile
+    // t-2.  K then has two steps to arrive and V three, and each step waits only for the loads
+    // issued two steps back: two tile sets in flight per workgroup instead of one (cfg4 at
+    // D = 256: 3.71 -> 3.19 ms).  The two-head items of D = 128, whose streams are short, ran
+    // 4-6 % slower that way (cfg1, cfg2) and keep the one-ahead ring.
+    constexpr bool SPLIT = NS == 4 && D == 256;
     constexpr int LPTK = D == 256 ? HD::kParts : HPW;   // K loads per tile and wave (SPLIT)
     constexpr int WAIT_STEP = SPLIT ? LPT : (NS - 4) * LPT;   // loads a step may leave in flight
 
@@ -982,12 +984,11 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                             if (HPW == 1) {
                                 if (sl == 4) fast_issue_k(nt, ds, 0);
                                 if (sl == 8) fast_issue_v(nt, ds, 0);
-                                if (sl == 12) fast_advance();
                             } else {
-                                if (sl == 3 || sl == 5) fast_issue_v(nt, ds, (sl - 3) >> 1);
-                                if (sl == 7 || sl == 9) fast_issue_k(nt, dks, (sl - 7) >> 1);
-                                if (sl == 12) fast_shift();
+                                if (sl == 3 || sl == 5) fast_issue_k(nt, ds, (sl - 3) >> 1);
+                                if (sl == 7 || sl == 9) fast_issue_v(nt, ds, (sl - 7) >> 1);
                             }
+                            if (sl == 12) fast_advance();
                         } else {
                             if (sl == 2 || (HPW == 2 && sl == 4)) fast_issue_kv(nt, ds, (sl - 2) >> 1);
                             if (sl == 6) fast_advance();
@@ -1065,9 +1066,9 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
             if (t >= nt) break;
             wait_vmcnt<WAIT_STEP>();
             __syncthreads();
-            // DMA of tile t+NS-2 into the retired stage, spread over the step's slots.  SPLIT:
-            // V and ancestor words of tile t+NS-2 (described in the previous step) into the
-            // stage retired by P.V of tile t-2, then K of tile t+NS-1 into the stage of tile t-1.
+            // DMA of tile t+NS-2 into the retired stage, spread over the step's slots.  SPLIT
+            // (D = 256): V and ancestor words of tile t+NS-2 (described in the previous step) into
+            // the stage retired by P.V of tile t-2, then K of tile t+NS-1 into the stage of tile t-1.
             const int ds = (b + NS - 2) % NS;
             const int dks = (b + NS - 1) % NS;
             auto piece = [&](int sl) {
@@ -1084,19 +1085,16 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                     if (sl == 17) issue_k_part(IntTag<3>{}, dks);
                     if (sl == 22) pf = fetch(t + NS);
                 } else if constexpr (D == 128) {
+                    if (sl == 1) describe(t + NS - 2, pf);
                     if (HPW == 1) {
-                        if (sl == 1) describe(t + NS - 2, pf);
                         if (sl == 4) issue_k(ds, 0);
                         if (sl == 8) issue_v(ds, 0);
-                        if (sl == 12) issue_mask(ds);
-                        if (sl == 13) pf = fetch(t + NS - 1);
                     } else {
-                        if (sl == 1 || sl == 3) issue_v(ds, (sl - 1) >> 1);
-                        if (sl == 4) issue_mask(ds);
-                        if (sl == 5) describe(t + NS - 1, pf);
-                        if (sl == 7 || sl == 9) issue_k(dks, (sl - 7) >> 1);
-                        if (sl == 13) pf = fetch(t + NS);
+                        if (sl == 3 || sl == 5) issue_k(ds, (sl - 3) >> 1);
+                        if (sl == 7 || sl == 9) issue_v(ds, (sl - 7) >> 1);
                     }
+                    if (sl == 12) issue_mask(ds);
+                    if (sl == 13) pf = fetch(t + NS - 1);
                 } else {
                     if (sl == 1) describe(t + NS - 2, pf);
                     if (sl == 2 || (HPW == 2 && sl == 4)) issue_kv(ds, (sl - 2) >> 1);
