@@ -93,3 +93,51 @@ def assert_within_gate(actual: torch.Tensor, expected: dict, label: str, max_abs
     assert mx <= max_abs, f"{label}: max-abs {mx} > {max_abs}"
     assert mean <= mean_abs, f"{label}: mean-abs {mean} > {mean_abs}"
     return mx, mean
+
+
+def torch_fp32_rows(q, k_pool, v_pool, metadata, scale) -> torch.Tensor:
+    """Every packed row in float32 on the device: the semantics of paged_backend.py:116-213
+    restated with torch (prefix keys through the page table, tree keys through their scratch
+    slots and the ancestor bias, one softmax per row and query head).
+
+    An independent floating-point reference for full-size batches, where the fp64 oracle
+    can only take sampled rows; the tests pin it to that oracle on the sampled rows."""
+    block = metadata.block_size
+    kv_heads, dim = int(k_pool.shape[2]), int(k_pool.shape[3])
+    groups = int(q.shape[1]) // kv_heads
+    k_rows = k_pool.reshape(-1, kv_heads, dim)
+    v_rows = v_pool.reshape(-1, kv_heads, dim)
+    bias = metadata.qq_bias
+    offsets = metadata.qq_bias_offsets.cpu().tolist()
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    for r in range(metadata.num_requests):
+        sl = metadata.request_slice(r)
+        n = sl.stop - sl.start
+        prefix = metadata.prefix_lengths[r]
+        table = torch.as_tensor(metadata.block_tables_host[r], dtype=torch.long, device=q.device)
+        pos = torch.arange(prefix, device=q.device)
+        slots = torch.cat([table[pos // block] * block + pos % block, metadata.tree_slots[sl].long()])
+        keys = k_rows.index_select(0, slots).float()          # [P + T, Hkv, D]
+        values = v_rows.index_select(0, slots).float()
+        tree_bias = bias[offsets[r]:offsets[r] + n * n].reshape(n, n).float()
+        row_bias = torch.cat([torch.zeros((n, prefix), device=q.device), tree_bias], dim=1)   # [T, P + T]
+        row_bias = row_bias.repeat_interleave(groups, dim=0)                                  # [T * G, P + T]
+        for h in range(kv_heads):
+            query = q[sl, h * groups:(h + 1) * groups, :].float().reshape(n * groups, dim)
+            scores = query @ keys[:, h, :].t().contiguous() * scale + row_bias
+            probs = torch.softmax(scores, dim=-1)
+            result = probs @ values[:, h, :].contiguous()
+            out[sl, h * groups:(h + 1) * groups, :] = result.reshape(n, groups, dim)
+    return out
+
+
+def assert_within_gate_dense(actual: torch.Tensor, expected: torch.Tensor, label: str, max_abs=MAX_ABS,
+                             mean_abs=MEAN_ABS):
+    """The north-star gate over every element of two [rows, heads, dim] tensors on one device."""
+    diff = (actual.float() - expected.float()).abs()
+    mx, mean = float(diff.max()), float(diff.mean())
+    print(f"[{label}] every row: max-abs {mx:.3e} mean-abs {mean:.3e} over {actual.shape[0]} rows", flush=True)
+    assert np.isfinite(mx), f"{label}: non-finite output"
+    assert mx <= max_abs, f"{label}: max-abs {mx} > {max_abs}"
+    assert mean <= mean_abs, f"{label}: mean-abs {mean} > {mean_abs}"
+    return mx, mean

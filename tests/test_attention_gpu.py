@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from gpu_helpers import assert_within_gate, oracle_rows
+from gpu_helpers import assert_within_gate, assert_within_gate_dense, oracle_rows, torch_fp32_rows
 from jetspec_amd import (PackedTreeMetadata, packed_tree_attention, packed_tree_attention_prefix_prevalidated,
                          read_and_clear_status, workloads)
 
@@ -254,6 +254,24 @@ def test_large_configs_sampled_rows(config):
     expect = oracle_rows(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, requests, rows_per_request=4)
     assert_within_gate(out, expect, f"{config} sampled rows")
     assert read_and_clear_status(batch.q.device) == 0
+
+
+@pytest.mark.parametrize("config", ["config4", "config5"])
+def test_large_configs_every_row_vs_torch_fp32(config):
+    """Every row of the full-size batch against a float32 torch restatement of the reference
+    semantics on the GPU (gpu_helpers.torch_fp32_rows).  That restatement is first pinned to
+    the fp64 oracle on sampled rows of three requests (max-abs 1e-4), then the kernel's bf16
+    output is held to the north-star gate on all rows."""
+    batch = getattr(workloads, config)(DEV)
+    meta = batch.metadata
+    out = packed_tree_attention(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, 4)
+    reference = torch_fp32_rows(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale)
+    torch.cuda.synchronize()
+    assert read_and_clear_status(batch.q.device) == 0
+    requests = [0, meta.num_requests // 2, meta.num_requests - 1]
+    pins = oracle_rows(batch.q, batch.k_pool, batch.v_pool, meta, batch.scale, requests, rows_per_request=3)
+    assert_within_gate(reference, pins, f"{config} torch fp32 vs fp64 oracle", max_abs=1e-4, mean_abs=1e-5)
+    assert_within_gate_dense(out, reference, f"{config} kernel vs torch fp32")
 
 
 def test_greedy_acceptance_identical_to_oracle():
