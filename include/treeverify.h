@@ -266,6 +266,8 @@ int tv_truncate_accepted(const int32_t* paths, int32_t path_stride, const int32_
  *   chunk_keys: 0 = automatic; > 0 forces every prefix chunk to that many keys
  *               (a multiple of 32), which makes per-request results independent
  *               of the rest of the batch.
+ * Each request has 1 to 2048 tree nodes (a work item caches its tree's scratch slots in
+ * LDS); larger trees return TV_ERR_UNSUPPORTED and run tv_tree_attention_fp32.
  * An item is 8 int32: request, first KV head, first node, prefix key begin, key end,
  * flags, partial-result slot (-1: unsplit), KV heads per item.  Flags: bit 0 = last
  * prefix chunk (that item also covers the tree), bit 1 = last node block of its
@@ -296,7 +298,7 @@ int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int32_t* node_
 /*
  * The plan of a slot-addressed launch (tv_tree_attention_args.prefix_slots set): the same
  * items, with every prefix chunk at most 2048 keys (the keys' slots are cached per work
- * item) and no page-size constraint.  Replaces the grid of the legacy single-request
+ * item, beside at most 1024 tree nodes per request) and no page-size constraint.  Replaces the grid of the legacy single-request
  * kernel, paged_backend.py:343-348.
  */
 int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
@@ -338,7 +340,7 @@ int tv_tree_attention_plan_device(const int32_t* prefix_lens, const int32_t* nod
  * qq_bias element count), whatever the individual node counts.  The reference's
  * PackedTargetGraph replays one captured graph for all of them (target_graph.py:150-167),
  * so a captured launch must be sized for the whole class:
- *     max T <= min(1024, Q - (R - 1), floor(sqrt(sum T^2)))
+ *     max T <= min(2048, Q - (R - 1), floor(sqrt(sum T^2)))
  *     node blocks <= Hkv * min((Q + (N - 1) R) / N, R * ceil(max T / N)),
  * N = 256 / queries_per_kv nodes per one-head work item.
  */
@@ -488,8 +490,9 @@ int64_t tv_tree_attention_workspace_bytes(int32_t num_partial_slots, int32_t hea
  * which its dispatcher runs for every batch outside its fast kernel's geometry
  * (paged_backend.py:288-306), and of the legacy slot-addressed kernel
  * (paged_backend.py:20-113).  Replaces them where tv_tree_attention's MFMA kernel does
- * not apply: f32 operands, head sizes other than 128 (1..512), any number of query heads
- * per KV head, page sizes that are not multiples of 32, trees above 1024 nodes, and
+ * not apply: f32 operands, head sizes other than 64, 128 and 256 (1..512), query-head groups
+ * the MFMA instances do not take (any number per KV head), page sizes that are not
+ * multiples of 32, trees above 2048 nodes (above 1024 beside slot-addressed prefixes), and
  * finite qq_bias values (added to the score, as the reference does).
  *
  * out[q, h, :] = sum_k p_k V[k, h/G, :] / sum_k p_k with p_k = exp(s_k - max s) and

@@ -101,10 +101,15 @@ constexpr int kMaskBytes = 8 * 64 * 4;                // per stage: each wave's 
 constexpr int kRingBytes = 8 * (2 * kTileBytes + kMaskBytes);
 constexpr int kMaxPages = 512;                        // page numbers of one prefix chunk
 constexpr int kMaxSlotChunk = 2048;                   // prefix keys of one chunk in slot addressing
-constexpr int kMaxTreeSlots = 1024;                   // tree slots cached per work item
+constexpr int kMaxTreeSlots = 1024;                   // tree slots cached per work item (slot-addressed prefix)
+constexpr int kMaxTreeNodes = 2048;                   // ... with a page-table prefix
 constexpr int kPagesOffset = kRingBytes;              // page numbers, or the chunk's prefix slots
 constexpr int kSlotsOffset = kPagesOffset + kMaxSlotChunk * 4;
 constexpr int kLdsBytes = kSlotsOffset + kMaxTreeSlots * 4;   // 159744 of gfx950's 160 KiB
+// With a page-table prefix only kMaxPages page numbers occupy the prefix region, so the tree
+// slots start right after them and run on through the slot region: kMaxTreeNodes of them.
+constexpr int kTreeSlotsPageOffset = kPagesOffset + kMaxPages * 4;
+static_assert(kTreeSlotsPageOffset + kMaxTreeNodes * 4 <= kLdsBytes, "page-mode tree slots exceed the LDS");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaxTileSum = 256.f;                  // per lane half, against the reference
 

@@ -240,7 +240,7 @@ int launch_tree_attention(const tv_tree_attention_args* a, void* stream) {
         ks[2] * 2 >= (int64_t{1} << 31) || vs[2] * 2 >= (int64_t{1} << 31)) {
         return fail(TV_ERR_UNSUPPORTED, "tree_attention: K/V strides out of range");
     }
-    if (a->ancestor_words_per_row < 1 || a->ancestor_words_per_row > kMaxTreeSlots / 64) {
+    if (a->ancestor_words_per_row < 1 || a->ancestor_words_per_row > kMaxTreeNodes / 64) {
         return fail(TV_ERR_INVALID, "tree_attention: ancestor_words_per_row %d out of range",
                     a->ancestor_words_per_row);
     }

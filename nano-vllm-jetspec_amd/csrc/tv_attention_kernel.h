@@ -313,7 +313,8 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
     // The planner keeps every item within the LDS page/slot caches, non-empty, inside its
     // request's prefix and inside the workspace; an item that is not (a plan made for other
     // metadata) is reported and skipped rather than read past the request's table row.
-    if (nt == 0 || npages > kMaxPages || tree_end > kMaxTreeSlots || (slot_mode && nkeys > kMaxSlotChunk) ||
+    if (nt == 0 || npages > kMaxPages || tree_end > (slot_mode ? kMaxTreeSlots : kMaxTreeNodes) ||
+        (slot_mode && nkeys > kMaxSlotChunk) ||
         it.h0 < 0 || it.n0 < 0 || it.kbeg < 0 || it.kend < it.kbeg || it.kend > plen || it.slot >= p.num_slots) {
         if (tid == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
@@ -321,13 +322,14 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
 
     // Page numbers of the prefix chunk and slots of the tree, validated, into LDS, and
     // this lane's Q rows into registers.  All of them are loaded before any is used
-    // (at most one page and two slots per thread), so the three lookups cost one round
-    // trip, not three.
+    // (at most one page and two tree slots per thread, four at D = 256), so the three
+    // lookups cost one round trip, not three.
     constexpr int PPT = (kMaxPages + THREADS - 1) / THREADS;       // page loads per thread
-    constexpr int TPT = (kMaxTreeSlots + THREADS - 1) / THREADS;   // tree slot loads per thread
+    constexpr int TPT = (kMaxTreeSlots + THREADS - 1) / THREADS;   // tree slot loads per thread (first 1024)
+    constexpr int XPT = (kMaxTreeNodes - kMaxTreeSlots + THREADS - 1) / THREADS;   // ... beyond them
     constexpr int SPT = (kMaxSlotChunk + THREADS - 1) / THREADS;   // prefix slot loads per thread
     int32_t* pages = reinterpret_cast<int32_t*>(smem + kPagesOffset);
-    int32_t* tslots = reinterpret_cast<int32_t*>(smem + kSlotsOffset);
+    int32_t* tslots = reinterpret_cast<int32_t*>(smem + (slot_mode ? kSlotsOffset : kTreeSlotsPageOffset));
     int32_t pg[PPT];
     int64_t sl[TPT];
     int64_t ps[SPT];
@@ -401,6 +403,22 @@ __device__ __forceinline__ void run_item(const AttnParams& p, char* smem, const 
                 v = 0;
             }
             tslots[i] = static_cast<int32_t>(v);
+        }
+    }
+    // Trees above 1024 nodes (page-table prefixes only): their further slots in a second round
+    // trip, so the common prologue keeps its one.
+    if (tree_end > kMaxTreeSlots) {
+#pragma unroll
+        for (int k = 0; k < XPT; ++k) {
+            const int i = kMaxTreeSlots + tid + k * THREADS;
+            if (i < tree_end) {
+                int64_t v = p.tree_slots[qbase + i];
+                if (v < 0 || v >= pool_slots) {
+                    set_status(p.status, TV_STATUS_BAD_PAGE);
+                    v = 0;
+                }
+                tslots[i] = static_cast<int32_t>(v);
+            }
         }
     }
     // Retire the Q loads here: the tile loop then contains no compiler-tracked vector

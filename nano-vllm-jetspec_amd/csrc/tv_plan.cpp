@@ -30,7 +30,8 @@ constexpr int kHeadDim = 128;
 constexpr int kMinChunkKeys = 64;   // shortest prefix chunk worth a partial result
 constexpr int kMaxChunkPages = 512; // page numbers a workgroup caches in LDS
 constexpr int kMaxSlotChunk = 2048; // prefix slots a workgroup caches in LDS (slot addressing)
-constexpr int kMaxTreeNodes = 1024; // tree slots a workgroup caches in LDS
+constexpr int kMaxTreeNodes = 2048; // tree slots a workgroup caches in LDS (page-table prefixes)
+constexpr int kMaxTreeNodesSlots = 1024;   // ... beside a slot-addressed prefix chunk
 constexpr int64_t kFillRounds = 4;  // item rounds the chunk target is refitted for
 
 struct Item {
@@ -157,7 +158,7 @@ void place_for_xcds(std::vector<Item>& items) {
 // The plan for chunks of at most max_chunk keys (a multiple of 32).
 int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32_t num_requests,
          int32_t num_kv_heads, int32_t qpk, int32_t num_compute_units, int32_t chunk_keys, int64_t max_chunk,
-         int32_t* items_host, int32_t* groups_host, tv_attention_plan_info* info) {
+         int32_t max_tree_nodes, int32_t* items_host, int32_t* groups_host, tv_attention_plan_info* info) {
     if (!info || !prefix_lens_host || !node_counts_host) return fail(TV_ERR_INVALID, "plan: null argument");
     if (num_requests < 1) return fail(TV_ERR_INVALID, "plan: at least one request is required");
     if (num_kv_heads < 1) return fail(TV_ERR_INVALID, "plan: num_kv_heads must be positive");
@@ -174,9 +175,9 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
         const int32_t p = prefix_lens_host[r], t = node_counts_host[r];
         if (p < 0) return fail(TV_ERR_INVALID, "plan: negative prefix length for request %d", r);
         if (t < 1) return fail(TV_ERR_INVALID, "plan: request %d has no tree nodes", r);
-        if (t > kMaxTreeNodes) {
+        if (t > max_tree_nodes) {
             return fail(TV_ERR_UNSUPPORTED, "plan: request %d has %d tree nodes (at most %d per request)", r, t,
-                        kMaxTreeNodes);
+                        max_tree_nodes);
         }
         max_nodes = std::max(max_nodes, t);
         const int hpw = heads_per_group(t, num_kv_heads, qpk);
@@ -323,7 +324,7 @@ extern "C" int tv_tree_attention_plan(const int32_t* prefix_lens_host, const int
     // Longest chunk whose pages fit the LDS page cache wherever it starts.
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
     return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, queries_per_kv, num_compute_units,
-                chunk_keys, max_chunk, items_host, groups_host, info);
+                chunk_keys, max_chunk, kMaxTreeNodes, items_host, groups_host, info);
 }
 
 extern "C" int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t* node_counts_host,
@@ -333,5 +334,5 @@ extern "C" int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, con
                                             tv_attention_plan_info* info) {
     clear_error();
     return plan(prefix_lens_host, node_counts_host, num_requests, num_kv_heads, queries_per_kv, num_compute_units,
-                chunk_keys, kMaxSlotChunk, items_host, groups_host, info);
+                chunk_keys, kMaxSlotChunk, kMaxTreeNodesSlots, items_host, groups_host, info);
 }

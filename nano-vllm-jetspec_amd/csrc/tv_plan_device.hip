@@ -30,6 +30,7 @@ namespace {
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxSortItems = 8192;      // LDS sort capacity (64 KiB of keys)
 constexpr int kMaxPlanRequests = 2048;
+constexpr int kMaxPlanNodes = 2048;     // tree nodes of one request (the attention kernel's page-mode cache)
 constexpr int kMinChunkKeys = 64;
 constexpr int kMaxChunkPages = 512;
 constexpr int kXcds = 8;
@@ -171,8 +172,8 @@ plan_device_kernel(const PlanArgs a) {
     int64_t my_cost = 0;
     for (int r = t; r < R; r += kPlanThreads) {
         const int p = a.prefix_lens[r], n = a.node_counts[r];
-        bad |= p < 0 || n < 1 || n > 1024;
-        const int pc = max(0, p), nc = max(1, min(1024, n));
+        bad |= p < 0 || n < 1 || n > kMaxPlanNodes;
+        const int pc = max(0, p), nc = max(1, min(kMaxPlanNodes, n));
         req_p[r] = pc;
         req_n[r] = nc;
         const ReqShape s = req_shape(nc, KV, NW);
@@ -594,7 +595,9 @@ extern "C" int tv_tree_attention_plan_capacity(const int32_t* node_counts_host, 
     int32_t max_nodes = 1;
     for (int32_t r = 0; r < num_requests; ++r) {
         const int32_t n = node_counts_host[r];
-        if (n < 1 || n > 1024) return fail(TV_ERR_UNSUPPORTED, "plan_capacity: request %d has %d nodes", r, n);
+        if (n < 1 || n > kMaxPlanNodes) {
+            return fail(TV_ERR_UNSUPPORTED, "plan_capacity: request %d has %d nodes", r, n);
+        }
         max_nodes = n > max_nodes ? n : max_nodes;
         const int hpw = n <= nodes_per_item(2, qpk) && num_kv_heads >= 2 ? 2 : 1;
         const int npw = nodes_per_item(hpw, qpk);
@@ -626,7 +629,7 @@ extern "C" int tv_tree_attention_plan_capacity_packed(int32_t total_queries, int
         while ((root + 1) * (root + 1) <= sum_node_squares) ++root;
         max_nodes = std::min(max_nodes, root);
     }
-    max_nodes = std::min<int64_t>(max_nodes, 1024);
+    max_nodes = std::min<int64_t>(max_nodes, kMaxPlanNodes);
     // With N = nodes_per_item(1, qpk) nodes per one-head item (64 at qpk 4), a request of T
     // nodes has at most num_kv_heads * ceil(T / N) node blocks (two-head groups of smaller
     // trees have fewer), and sum_r ceil(T_r / N) is at most (Q + (N - 1) R) / N and at most

@@ -11,9 +11,10 @@ bf16/f16 products, fp32 accumulation and online softmax, in two probability mode
 relative (two MFMAs: its rounding and the rounding of the remainder) and sum it in
 fp32, the reference's "never BF16 probabilities" (paged_backend.py:248-256).
 
-Batches outside the MFMA kernel's geometry (f32 operands, head sizes other than 128 and
-64, query groups other than 1-8 and 16 (1, 2, 4, 8 and 16 at head size 64), page sizes
-that are not multiples of 32, trees above 1024 nodes, unaligned pools) run the FP32 kernel (tv_tree_attention_fp32), as the
+Batches outside the MFMA kernel's geometry (f32 operands, head sizes other than 64, 128
+and 256, query groups other than 1-8 and 16 (1, 2, 4, 8 and 16 at head sizes 64 and 256),
+page sizes that are not multiples of 32, trees above MFMA_MAX_TREE_NODES nodes, unaligned
+pools) run the FP32 kernel (tv_tree_attention_fp32), as the
 reference's dispatcher runs its scalar FP32 kernel outside its fast kernel's geometry
 (paged_backend.py:288-306).  It reads every metadata value from device memory, needs
 no plan, and is capturable as is.
@@ -116,6 +117,13 @@ def _aligned_rows(t: torch.Tensor) -> bool:
     return t.data_ptr() % 16 == 0 and all(t.stride(i) % 8 == 0 for i in range(t.ndim - 1))
 
 
+# Tree nodes per request the MFMA kernel takes with page-table prefixes (its work items
+# cache the tree's scratch slots in LDS; csrc/tv_attention.h kMaxTreeNodes), and beside the
+# legacy entry's slot-addressed prefixes (kMaxTreeSlots).
+MFMA_MAX_TREE_NODES = 2048
+MFMA_MAX_TREE_NODES_SLOTS = 1024
+
+
 def _mfma_geometry(q, k_pool, v_pool, metadata) -> bool:
     """True when the MFMA kernel (tv_tree_attention) takes this batch; the others run the
     FP32 kernel.  Mirrors the MFMA entry's limits (csrc/tv_attention.hip)."""
@@ -124,7 +132,7 @@ def _mfma_geometry(q, k_pool, v_pool, metadata) -> bool:
     kv_heads = int(k_pool.shape[2])
     if q.shape[1] % kv_heads or not mfma_head(int(q.shape[-1]), q.shape[1] // kv_heads):
         return False
-    if metadata.block_size % 32 or max(metadata.node_counts_host, default=0) > 1024:
+    if metadata.block_size % 32 or max(metadata.node_counts_host, default=0) > MFMA_MAX_TREE_NODES:
         return False
     if k_pool.stride(3) != 1 or v_pool.stride(3) != 1 or not _aligned_rows(k_pool) or not _aligned_rows(v_pool):
         return False
@@ -458,7 +466,8 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     With a 0 / -inf bias (what the reference's runners build) and the MFMA kernel's
     geometry, the MFMA kernel runs in slot-addressed mode with FP32 probabilities (the
     legacy kernel is the frozen FP32 one, paged_backend.py:20-113); anything else (finite
-    bias values, f32 operands, other head sizes or query groups, trees above 1024 nodes)
+    bias values, f32 operands, other head sizes or query groups, trees above 1024 nodes beside
+    the slot-addressed prefix)
     runs the FP32 kernel.  Like the reference, it reads the sequence length from the
     device (one synchronisation).  Multi-request calls are rejected exactly as in the
     reference; the block-table form without logical slots or bias runs the external
@@ -510,7 +519,7 @@ def paged_tree_attention(q, k_pool, v_pool, block_table, cu_seqlens_q, seq_lens_
     # is added to the score) takes the FP32 kernel.
     mask_bias = bool(((bias == 0) | (bias == float("-inf"))).all())
     geometry = (q.dtype != torch.float32 and mfma_head(head_size, num_queries_per_kv)
-                and total_q <= 1024 and k_pool.stride(3) == 1 and v_pool.stride(3) == 1
+                and total_q <= MFMA_MAX_TREE_NODES_SLOTS and k_pool.stride(3) == 1 and v_pool.stride(3) == 1
                 and _aligned_rows(k_pool) and _aligned_rows(v_pool)
                 and int(k_pool.shape[0]) * int(block_size) < (1 << 31))
     if mask_bias and geometry:

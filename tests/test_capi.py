@@ -384,6 +384,35 @@ def test_slot_plan_caps_prefix_chunks(prefix, nodes, kv_heads, groups, same):
         assert int((page_items[:, 4] - page_items[:, 3]).max()) > 2048
 
 
+@pytest.mark.parametrize("prefixes,counts,kv_heads", [
+    ([512, 3000], [2048, 16], 8), ([0], [1500], 2), ([9000, 100], [1025, 2048], 1)])
+def test_plan_covers_trees_up_to_2048_nodes(prefixes, counts, kv_heads):
+    """Page-table plans take trees of up to 2048 nodes (the kernel caches that many tree slots
+    beside 512 page numbers); the slot-addressed plan keeps 1024, its LDS also holding 2048
+    prefix slots."""
+    check_plan_covers(prefixes, counts, kv_heads, 256)
+
+
+def test_plan_rejects_trees_beyond_its_slot_caches():
+    lib = _lib.library()
+    info = _lib.PlanInfo()
+
+    def plan(entry, nodes):
+        prefixes, counts = (ctypes.c_int32 * 1)(64), (ctypes.c_int32 * 1)(nodes)
+        if entry == "page":
+            return lib.tv_tree_attention_plan(prefixes, counts, 1, 8, 4, 256, 256, 0, None, None, ctypes.byref(info))
+        return lib.tv_tree_attention_plan_slots(prefixes, counts, 1, 8, 4, 256, 0, None, None, ctypes.byref(info))
+
+    assert plan("page", 2048) == _lib.TV_OK and info.ancestor_words_per_row == 32
+    assert plan("page", 2049) == _lib.TV_ERR_UNSUPPORTED and b"2049 tree nodes" in lib.tv_last_error()
+    assert plan("slots", 1024) == _lib.TV_OK
+    assert plan("slots", 1025) == _lib.TV_ERR_UNSUPPORTED
+    assert _capacity(lib, (2048, 7), 8, 256, 256, 0, 20000).ancestor_words_per_row == 32
+    with pytest.raises(ValueError):
+        _capacity(lib, (2049,), 8, 256, 256, 0, 20000)
+    assert _capacity_packed(lib, (2048, 1), 8, 256, 256, 0, 20000).ancestor_words_per_row == 32
+
+
 def test_plan_at_benchmark_shapes():
     rng = np.random.default_rng(4)
     prefixes = [int(x) for x in rng.integers(8192, 32769, size=64)]
@@ -465,10 +494,11 @@ def test_signature_capacity_covers_every_node_count_vector():
     seeded random vectors and on pairs that share a signature."""
     lib = _lib.library()
     rng = np.random.default_rng(3)
-    vectors = [(12, 60, 72), (24, 36, 84), (1, 5, 6), (2, 3, 7), (64,) * 64, (1024,), (1, 1024), (33, 31)]
+    vectors = [(12, 60, 72), (24, 36, 84), (1, 5, 6), (2, 3, 7), (64,) * 64, (1024,), (1, 1024), (33, 31),
+               (2048,), (2048, 1), (1500, 600)]
     for _ in range(3000):
         count = int(rng.integers(1, 9))
-        high = int(rng.choice([40, 130, 300, 1024]))
+        high = int(rng.choice([40, 130, 300, 1024, 2048]))
         vectors.append(tuple(int(x) for x in rng.integers(1, high + 1, size=count)))
     cases = [(8, 0, 4), (1, 0, 4), (2, 0, 4), (8, 2048, 4), (8, 0, 1), (2, 0, 16), (1, 0, 8), (8, 2048, 2),
              (8, 0, 5), (2, 0, 7), (1, 2048, 3)]

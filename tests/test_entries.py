@@ -100,7 +100,7 @@ def test_legacy_entry_rejections_before_any_device_work():
 def test_kernel_choice_follows_the_mfma_geometry():
     """The drop-in's per-batch kernel choice (host logic): the MFMA kernel for bf16/f16,
     head_dim 128 with 1-8 or 16 query heads per KV head or head_dim 64 or 256 with 1, 2, 4, 8 or 16,
-    page sizes that are multiples of 32, trees of at most 1024 nodes and 16-byte aligned K/V
+    page sizes that are multiples of 32, trees of at most 2048 nodes and 16-byte aligned K/V
     rows; the FP32 kernel otherwise."""
     from types import SimpleNamespace
 
@@ -116,7 +116,7 @@ def test_kernel_choice_follows_the_mfma_geometry():
     assert case(dtype=torch.float16)
     for groups in (1, 2, 3, 5, 6, 7, 8, 16):
         assert case(groups=groups), groups
-    assert case(nodes=(1024, 3)) and case(block=32) and case(block=512)
+    assert case(nodes=(1024, 3)) and case(nodes=(2048, 1025)) and case(block=32) and case(block=512)
     assert not case(dtype=torch.float32)
     for groups in (9, 12, 32):
         assert not case(groups=groups), groups
@@ -128,7 +128,7 @@ def test_kernel_choice_follows_the_mfma_geometry():
     for head_dim in (32, 96, 512):
         assert not case(head_dim=head_dim), head_dim
     assert not case(block=16) and not case(block=48)
-    assert not case(nodes=(64, 1025))
+    assert not case(nodes=(64, 2049))
     wide = torch.zeros(4, 256, 8, 256, dtype=torch.bfloat16)
     assert not case(pool=wide[..., ::2])                     # strided head dimension
     assert not case(pool=wide[..., 1:129])                   # rows not 16-byte aligned

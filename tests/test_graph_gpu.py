@@ -1,7 +1,8 @@
 """Graph-capturable verify: the device planner and HIP-graph replay (GPU).
 
 * tv_tree_attention_plan_device writes the host planner's items and merge groups,
-  item for item, for the benchmark batches, ragged batches and forced chunk lengths.
+  item for item, for the benchmark batches, ragged batches (trees of up to 2048 nodes
+  among them) and forced chunk lengths.
 * GraphedTreeAttention (device plan, capacity grids, no allocation) equals
   packed_tree_attention bit for bit.
 * PackedVerifyGraph: one capture, then replays with new prefix lengths, page tables,
@@ -74,6 +75,7 @@ def batches():
     yield "cfg5", workloads.config5(DEV).metadata
     yield "ragged", ragged_metadata(1, [0, 1, 63, 64, 65, 255, 256, 257, 9000], [1, 2, 16, 17, 32, 33, 64, 65, 512])
     yield "long", ragged_metadata(2, [150000, 3], [64, 16])
+    yield "big", ragged_metadata(4, [3000, 0, 700], [2048, 1500, 16])
 
 
 def shard_batches():
@@ -117,7 +119,7 @@ def test_capacity_overflow_writes_zero_counts():
     assert counts.tolist() == [0, 0, 0, 1]
 
 
-@pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg5", "ragged"])
+@pytest.mark.parametrize("name", ["cfg1", "cfg2", "cfg5", "ragged", "big"])
 def test_graphed_attention_equals_eager(name):
     meta = dict(batches())[name]
     g = torch.Generator(device=DEV).manual_seed(4)
