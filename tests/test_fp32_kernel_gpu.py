@@ -134,10 +134,10 @@ def test_page_sizes_that_are_not_multiples_of_32(block):
     check(packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4), q, k, v, meta, f"B{block}")
 
 
-def test_causal_chunk_above_1024_nodes():
-    q, k, v, meta, *_ = make_case((2000, 100), (1500, 64), kv_heads=1, chain=True, seed=9)
+def test_causal_chunk_above_2048_nodes():
+    q, k, v, meta, *_ = make_case((2000, 100), (2100, 64), kv_heads=1, chain=True, seed=9)
     assert not _mfma_geometry(q, k, v, meta)
-    check(packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4), q, k, v, meta, "1500-row chunk",
+    check(packed_tree_attention(q, k, v, meta, 128 ** -0.5, 4), q, k, v, meta, "2100-row chunk",
           rows_per_request=24)
 
 

@@ -26,9 +26,11 @@ DEV = "cuda"
 EXACT_AGREEMENT = 5e-5
 
 
-def random_batch(seed):
+def random_batch(seed, big=False):
+    """A seeded random batch; `big` draws 1 to 4 requests, the first with a tree of 1025 to
+    2048 nodes (the MFMA kernel's large-tree range)."""
     rng = np.random.default_rng(seed)
-    requests = int(rng.integers(1, 49))
+    requests = int(rng.integers(1, 5)) if big else int(rng.integers(1, 49))
     block = int(rng.choice([32, 64, 128, 256, 512]))
     kv_heads = int(rng.choice([1, 2, 4, 8]))
     groups = int(rng.choice(SUPPORTED_GROUPS))
@@ -36,6 +38,9 @@ def random_batch(seed):
     prefixes = [int(x) for x in rng.integers(0, 40000 if requests < 16 else 12000, size=requests)]
     counts = [int(rng.choice([1, 7, 16, 24, 33, 48, 64, 96, 129, 256, 500, 1024])) if rng.random() < 0.9 else 1
               for _ in range(requests)]
+    if big:
+        counts[0] = int(rng.integers(1025, 2049))
+        prefixes = [min(p, 6000) for p in prefixes]
     parents = [workloads.random_parents(n, int(rng.integers(1, 12)), rng) if rng.random() < 0.7
                else workloads.chain_parents(n) for n in counts]
     prefix_pages = [-(-p // block) for p in prefixes]
@@ -80,6 +85,27 @@ def test_mfma_kernel_equals_fp32_kernel(seed):
     d_fast = (fast.float() - reference).abs()
     print(f"[crosscheck] exact max {d_exact.max().item():.2e} mean {d_exact.mean().item():.2e}; "
           f"bf16-P max {d_fast.max().item():.2e} mean {d_fast.mean().item():.2e}", flush=True)
+    assert d_exact.max().item() <= EXACT_AGREEMENT
+    assert d_fast.max().item() <= MAX_ABS and d_fast.mean().item() <= MEAN_ABS
+    assert read_and_clear_status(DEV) == 0
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_big_trees_mfma_kernel_equals_fp32_kernel(seed):
+    q, k, v, meta, groups, label = random_batch(9300 + seed, big=True)
+    print(f"[crosscheck big] {label}", flush=True)
+    assert _mfma_geometry(q, k, v, meta)
+    scale = 128 ** -0.5
+    stream = torch.cuda.current_stream().cuda_stream
+    reference = torch.empty(q.shape, dtype=torch.float32, device=DEV)
+    _launch_fp32(_fp32_template(meta, k, v, groups, q.device), q, reference, scale, stream)
+    exact = packed_tree_attention_reference(q, k, v, meta, scale, groups, output_dtype=torch.float32)
+    fast = packed_tree_attention(q, k, v, meta, scale, groups)
+    torch.cuda.synchronize()
+    d_exact = (exact - reference).abs()
+    d_fast = (fast.float() - reference).abs()
+    print(f"[crosscheck big] exact max {d_exact.max().item():.2e}; bf16-P max {d_fast.max().item():.2e} "
+          f"mean {d_fast.mean().item():.2e}", flush=True)
     assert d_exact.max().item() <= EXACT_AGREEMENT
     assert d_fast.max().item() <= MAX_ABS and d_fast.mean().item() <= MEAN_ABS
     assert read_and_clear_status(DEV) == 0
