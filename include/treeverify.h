@@ -470,7 +470,8 @@ typedef struct tv_tree_attention_args {
  * 1..8 or 16, or head_dim 64 or 256 and G in 1, 2, 4, 8, 16 (the reference's grouped
  * kernel takes powers of two up to 16 and pads the head size to a power of two,
  * tree_gqa.py:124-135; its FP32 kernel any geometry, as tv_tree_attention_fp32 does),
- * block_size % 32 == 0 (any positive block_size with prefix_slots).  The plan must
+ * block_size % 32 == 0 (any positive block_size with prefix_slots), at most 2048 tree
+ * nodes per request (1024 with prefix_slots) and ancestor_words_per_row <= 32.  The plan must
  * have been made for the same G; plans do not depend on head_dim.  workspace_bytes must
  * be at least tv_tree_attention_workspace_bytes(num_partial_slots, head_dim).
  */
