@@ -63,9 +63,10 @@ def parse_args():
     parser.add_argument("--head-dim", type=int, default=128, choices=(64, 128, 256),
                         help="head size of the batch (128 in the Qwen3 geometry); 64 and 256 run the MFMA "
                              "kernel's instances for those sizes, measured on the verify step only")
-    parser.add_argument("--legs", choices=("all", "verify"), default="all",
+    parser.add_argument("--legs", choices=("all", "verify", "graph"), default="all",
                         help="'verify' measures only the verify step (for a kernel profile of exactly the timed "
-                             "launches); 'all' adds the rope_scatter, accept, graph and exact legs")
+                             "launches); 'graph' adds only the graph leg (a profile of the replayed round, device "
+                             "planner included); 'all' adds the rope_scatter, accept, graph, exact and round legs")
     parser.add_argument("--operands", choices=("normal", "constant", "zero", "zero-q", "zero-kv"), default="normal",
                         help="diagnostic: replace the N(0,1) Q/K/V values by constants or zeros (same shapes, "
                              "pages, trees, instructions and bytes) to show the part's data-dependent clock; "
@@ -595,12 +596,14 @@ def run_verify(args, torch):
         result["config"]["shard"] = f"tensor-parallel shard: {batch.kv_heads} of 8 KV heads"
     if args.groups != 4:
         result["config"]["geometry"] = f"{args.groups} query heads per KV head"
-    if args.legs == "all" and args.kv_heads == 8 and args.groups == 4 and args.head_dim == 128:
-        result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
-        result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
+    if args.legs != "verify" and args.kv_heads == 8 and args.groups == 4 and args.head_dim == 128:
+        if args.legs == "all":
+            result["rope_scatter"] = rope_leg(batch, torch, args.steps, args.warmup)
+            result["accept"] = accept_leg(batch, torch, args.steps, args.warmup)
         result["graph"] = graph_leg(batch, torch, args.steps, args.warmup)
-        result["exact"] = exact_leg(batch, torch, args.steps, args.warmup)
-        result["round"] = round_leg(batch, torch, rounds=3 if args.config == 4 else 5)
+        if args.legs == "all":
+            result["exact"] = exact_leg(batch, torch, args.steps, args.warmup)
+            result["round"] = round_leg(batch, torch, rounds=3 if args.config == 4 else 5)
     if args.sustain > 0:
         result["sustained"] = sustain_leg(batch, torch, args.sustain)
     probe = copy_probe(torch)

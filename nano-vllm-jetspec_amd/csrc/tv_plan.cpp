@@ -216,7 +216,9 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
     if (chunk_keys == 0) {
         const int64_t now = items_for(target);
         const int64_t rounds = (now + num_compute_units - 1) / num_compute_units;
-        if (now > num_compute_units && rounds <= kFillRounds) {
+        // Rounds already full: every smaller target that keeps the item count keeps every
+        // request's chunk count (each is non-increasing in the target), so the plan is this one.
+        if (now > num_compute_units && rounds <= kFillRounds && now < rounds * num_compute_units) {
             int64_t lo = 1, hi = target;   // items_for(hi) fits `rounds` full rounds
             while (lo < hi) {
                 const int64_t mid = lo + (hi - lo) / 2;
