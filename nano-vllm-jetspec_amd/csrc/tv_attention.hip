@@ -104,7 +104,14 @@ merge_partials_kernel(const AttnParams p) {
     for (int group = blockIdx.x; group < count; group += gridDim.x) merge_group<T>(p, group);
 }
 
-__global__ void __launch_bounds__(256)
+// One thread per (row, word) of the ancestor bits.  Row i of a tree of tn nodes carries bits
+// for its elements m <= i; the word's elements that do (lim of them) are loaded without
+// conditions, every load clamped into that range so that all 64 issue back to back, then
+// masked.  Elements past the node or past the tree are not read; any element at or before
+// the node that is neither 0 nor -inf sets TV_STATUS_BAD_BIAS.
+constexpr int kPackThreads = 256;
+
+__global__ void __launch_bounds__(kPackThreads)
 pack_ancestor_kernel(const float* __restrict__ bias, const int64_t* __restrict__ bias_off,
                      const int32_t* __restrict__ q2r, const int32_t* __restrict__ local,
                      const int32_t* __restrict__ counts, int32_t total_q, int32_t num_requests, int32_t words,
@@ -121,20 +128,21 @@ pack_ancestor_kernel(const float* __restrict__ bias, const int64_t* __restrict__
         const int i = local[q];
         const int tn = counts[r];
         if (i >= 0 && i < tn) {
-            const float* row = bias + bias_off[r] + static_cast<int64_t>(i) * tn;
-            bool other = false;   // a value bits cannot carry
-            for (int b = 0; b < 64; ++b) {
-                const int m = 64 * w + b;
-                if (m < tn && m <= i) {
-                    const float x = row[m];
-                    if (x == 0.f) {
-                        word |= 1ull << b;
-                    } else if (x != -INFINITY) {
-                        other = true;
-                    }
+            const int lim = min(tn, i + 1) - 64 * w;   // elements of this word that carry bits
+            if (lim > 0) {
+                const float* seg = bias + bias_off[r] + static_cast<int64_t>(i) * tn + 64 * w;
+                float x[64];
+#pragma unroll
+                for (int b = 0; b < 64; ++b) x[b] = seg[min(b, lim - 1)];
+                bool other = false;   // a value bits cannot carry
+#pragma unroll
+                for (int b = 0; b < 64; ++b) {
+                    const bool in = b < lim;
+                    word |= static_cast<uint64_t>(in && x[b] == 0.f) << b;
+                    other |= in && x[b] != 0.f && x[b] != -INFINITY;
                 }
+                if (other) set_status(status, TV_STATUS_BAD_BIAS);
             }
-            if (other) set_status(status, TV_STATUS_BAD_BIAS);
         } else {
             set_status(status, TV_STATUS_BAD_REQUEST);
         }
@@ -160,8 +168,9 @@ extern "C" int tv_pack_ancestor_words(const float* qq_bias, const int64_t* qq_bi
         return fail(TV_ERR_INVALID, "pack_ancestor_words: null pointer");
     }
     const int64_t n = static_cast<int64_t>(total_queries) * words_per_row;
-    const int64_t blocks = (n + 255) / 256;
-    hipLaunchKernelGGL(pack_ancestor_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), qq_bias,
+    const int64_t blocks = (n + kPackThreads - 1) / kPackThreads;
+    hipLaunchKernelGGL(pack_ancestor_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kPackThreads), 0,
+                       as_stream(stream), qq_bias,
                        qq_bias_offsets, query_to_request, query_local_row, node_counts, total_queries,
                        num_requests, words_per_row, words, status);
     return check_launch("pack_ancestor_words");

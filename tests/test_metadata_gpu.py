@@ -8,7 +8,10 @@ the device from the parent arrays.  Checked against what they must equal:
   * every field of the validating constructor build() on the same requests,
     qq_bias bit for bit (packed_metadata.py:36-126 vs :128-199);
   * the attention output through either constructor's metadata, bit for bit;
-  * malformed parents are reported, not walked.
+  * malformed parents are reported, not walked;
+  * tv_pack_ancestor_words (the bits read back from a caller's qq_bias, as graph capture
+    does) equals the same packed masks, ignores entries above the diagonal, and reports a
+    value that bits cannot carry.
 """
 from __future__ import annotations
 
@@ -71,6 +74,49 @@ def test_words_equal_packed_oracle_masks():
         want = packed_words(oracle.mask_from_parents(parents), per_row)
         assert np.array_equal(got[sl], want), f"request {r} ({len(parents)} nodes)"
     assert read_and_clear_status(DEV) == 0
+
+
+def pack_from_bias(meta, per_row):
+    lib = _lib.library()
+    words = torch.full((meta.total_queries, per_row), -1, dtype=torch.int64, device=DEV)
+    status = torch.zeros(1, dtype=torch.int32, device=DEV)
+    _lib.check(lib.tv_pack_ancestor_words(meta.qq_bias.data_ptr(), meta.qq_bias_offsets.data_ptr(),
+                                          meta.query_to_request.data_ptr(), meta.query_local_row.data_ptr(),
+                                          meta.node_counts.data_ptr(), meta.total_queries, meta.num_requests, per_row,
+                                          words.data_ptr(), status.data_ptr(), _device.stream_handle(words.device)),
+               "pack_ancestor_words")
+    return words.cpu().numpy().view(np.uint64), int(status)
+
+
+def test_words_packed_from_bias_equal_packed_oracle_masks():
+    parent_lists = cases()
+    counts = [len(p) for p in parent_lists]
+    masks = [torch.from_numpy(oracle.mask_from_parents(p)).to(DEV) for p in parent_lists]
+    scratch = list(range(100, 100 + (sum(counts) + 255) // 256))
+    slots, offset = [], 0
+    for n in counts:
+        slots.append(torch.tensor([scratch[(offset + j) // 256] * 256 + (offset + j) % 256 for j in range(n)],
+                                  device=DEV))
+        offset += n
+    meta = PackedTreeMetadata.build([0] * len(counts), [[]] * len(counts), slots, masks, 256)
+    for per_row in (16, 17):   # the widest tree's words, and one spare word that must stay zero
+        got, status = pack_from_bias(meta, per_row)
+        assert status == 0
+        for r, parents in enumerate(parent_lists):
+            want = packed_words(oracle.mask_from_parents(parents), per_row)
+            assert np.array_equal(got[meta.request_slice(r)], want), f"request {r} ({len(parents)} nodes)"
+    # An entry above the diagonal carries no bit whatever it holds; one at or below it that is
+    # neither 0 nor -inf is reported.
+    r = 5   # the 200-node random tree
+    base = int(meta.qq_bias_offsets[r])
+    n = counts[r]
+    meta.qq_bias[base + 3 * n + 150] = 0.0
+    got, status = pack_from_bias(meta, 16)
+    assert status == 0
+    assert np.array_equal(got[meta.request_slice(r)], packed_words(oracle.mask_from_parents(parent_lists[r]), 16))
+    meta.qq_bias[base + 150 * n + 100] = 0.5
+    _, status = pack_from_bias(meta, 16)
+    assert status == _lib.TV_STATUS_BAD_BIAS
 
 
 def test_serving_constructor_equals_validating_constructor():
