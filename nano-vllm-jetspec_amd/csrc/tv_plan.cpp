@@ -63,6 +63,14 @@ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 // two-head chunks at half the length of one-head chunks of the same cost.
 int64_t cost_weight(int hpw) { return hpw == 2 ? 5 : 4; }
 
+// A tree tile takes the general loop (ancestor masks, per-key slot addresses) and costs
+// about two prefix tiles (per-workgroup timestamps on config 2: 16.3 us for the last-chunk
+// items of 64-node trees, 11 prefix tiles + 2 tree tiles, against 13.2 us for 12 prefix
+// tiles).  The chunk lengths of a split prefix are set so that the last chunk, which also
+// walks the tree, ends level with the others: the prefix is cut as if it held this many
+// keys per tree node more, within the same number of chunks.
+constexpr int64_t kTreeKeyWeight = 2;
+
 // MI355X dispatches workgroup i of a launch to XCD i % 8, and each XCD has its own L2.
 // The node blocks of one (request, head group, prefix chunk) stream the same K/V, and
 // in longest-first order they sit next to each other, so they would land on different
@@ -191,13 +199,20 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
         return fail(TV_ERR_INVALID, "plan: chunk_keys %d exceeds %lld", chunk_keys, (long long)max_chunk);
     }
 
-    // Chunk length of a prefix of p keys (hpw heads per item) for chunk target `tau`
-    // (in cost units): the longest multiple of 32 keys whose cost is not above tau,
-    // then equalised over the chunks.
-    auto chunk_for = [&](int64_t p, int hpw, int64_t tau) -> int64_t {
+    // Chunk length of a prefix of p keys before a tree of t nodes (hpw heads per item) for
+    // chunk target `tau` (in cost units): the longest multiple of 32 keys whose cost is not
+    // above tau gives the chunk count; the chunks then share the prefix and the tree's
+    // weight (kTreeKeyWeight keys a node) evenly, in multiples of 32 keys, as far as that
+    // keeps the chunk count (the chunks before the last stay below the prefix) and the cap.
+    auto chunk_for = [&](int64_t p, int64_t t, int hpw, int64_t tau) -> int64_t {
         int64_t chunk = std::min(round_up(std::max<int64_t>(kMinChunkKeys, tau / cost_weight(hpw)), 32), max_chunk);
         const int64_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1;
         chunk = round_up((p + nchunks - 1) / std::max<int64_t>(nchunks, 1), 32);
+        if (nchunks > 1) {
+            const int64_t even = round_up((p + kTreeKeyWeight * t + nchunks - 1) / nchunks, 32);
+            const int64_t keep = std::min((p - 1) / (nchunks - 1) / 32 * 32, max_chunk);
+            chunk = std::max(chunk, std::min(even, keep));
+        }
         return chunk < 32 ? 32 : chunk;
     };
     auto items_for = [&](int64_t tau) -> int64_t {
@@ -207,7 +222,7 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
             const int hpw = heads_per_group(node_counts_host[r], num_kv_heads, qpk);
             const int npw = nodes_per_item(hpw, qpk);
             const int64_t units = static_cast<int64_t>((num_kv_heads + hpw - 1) / hpw) * ((node_counts_host[r] + npw - 1) / npw);
-            const int64_t chunk = chunk_for(p, hpw, tau);
+            const int64_t chunk = chunk_for(p, node_counts_host[r], hpw, tau);
             n += units * (p > 0 ? (p + chunk - 1) / chunk : 1);
         }
         return n;
@@ -236,7 +251,7 @@ int plan(const int32_t* prefix_lens_host, const int32_t* node_counts_host, int32
         const int npw = nodes_per_item(hpw, qpk);
         const int32_t groups = (num_kv_heads + hpw - 1) / hpw;
         const int32_t blocks = (t + npw - 1) / npw;
-        const int64_t chunk = chunk_keys > 0 ? chunk_keys : chunk_for(p, hpw, tau);
+        const int64_t chunk = chunk_keys > 0 ? chunk_keys : chunk_for(p, t, hpw, tau);
         const int32_t nchunks = p > 0 ? static_cast<int32_t>((p + chunk - 1) / chunk) : 1;
         for (int32_t hg = 0; hg < groups; ++hg) {
             for (int32_t nb = 0; nb < blocks; ++nb) {

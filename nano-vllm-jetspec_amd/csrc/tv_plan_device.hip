@@ -182,14 +182,23 @@ __device__ __forceinline__ int div_small(int a, int b, int& rem) {
     return q;
 }
 
-// The host planner's chunk length (tv_plan.cpp, chunk_for) for a prefix of p keys, with
-// q = tau / cost_weight(hpw) precomputed: min(round_up(max(64, q), 32), max_chunk), then
-// equalised over the chunks.  Every quantity after the first min is below 2^32.
-__device__ __forceinline__ uint32_t chunk_of(uint32_t p, int64_t q, int64_t max_chunk) {
+// The host planner's chunk length (tv_plan.cpp, chunk_for) for a prefix of p keys before
+// a tree of n nodes, with q = tau / cost_weight(hpw) precomputed: the chunk count from
+// min(round_up(max(64, q), 32), max_chunk), then the prefix and the tree's weight shared
+// evenly over the chunks as far as the count and the cap allow.  Every quantity after the
+// first min is below 2^32.
+constexpr uint32_t kTreeKeyWeight = 2;   // prefix keys a tree node costs (tv_plan.cpp)
+
+__device__ __forceinline__ uint32_t chunk_of(uint32_t p, uint32_t n, int64_t q, int64_t max_chunk) {
     const int64_t c0 = min(round_up(max(static_cast<int64_t>(kMinChunkKeys), min(q, max_chunk)), 32), max_chunk);
     const uint32_t c = static_cast<uint32_t>(c0);
     const uint32_t nchunks = p > 0 ? (p + c - 1) / c : 1;
-    const uint32_t chunk = ((p + nchunks - 1) / nchunks + 31) / 32 * 32;
+    uint32_t chunk = ((p + nchunks - 1) / nchunks + 31) / 32 * 32;
+    if (nchunks > 1) {
+        const uint32_t even = ((p + kTreeKeyWeight * n + nchunks - 1) / nchunks + 31) / 32 * 32;
+        const uint32_t keep = min((p - 1) / (nchunks - 1) / 32 * 32, static_cast<uint32_t>(max_chunk));
+        chunk = max(chunk, min(even, keep));
+    }
     return chunk < 32 ? 32 : chunk;
 }
 
@@ -237,7 +246,7 @@ plan_device_kernel(const PlanArgs a) {
     auto request_items = [&](int r, int64_t q4, int64_t q5) -> int64_t {
         const uint32_t p = static_cast<uint32_t>(req_p[r]);
         const ReqShape s = shape_at(r);
-        const uint32_t chunk = chunk_of(p, s.hpw == 2 ? q5 : q4, max_chunk);
+        const uint32_t chunk = chunk_of(p, static_cast<uint32_t>(req_n[r]), s.hpw == 2 ? q5 : q4, max_chunk);
         return static_cast<int64_t>(s.G) * s.NB * (p > 0 ? (p + chunk - 1) / chunk : 1u);
     };
 
@@ -325,7 +334,8 @@ plan_device_kernel(const PlanArgs a) {
                 const uint32_t p = static_cast<uint32_t>(req_p[r]);
                 const ReqShape s = shape_at(r);
                 const uint32_t chunk = a.chunk_keys > 0 ? static_cast<uint32_t>(a.chunk_keys)
-                                                        : chunk_of(p, s.hpw == 2 ? q5 : q4, max_chunk);
+                                                        : chunk_of(p, static_cast<uint32_t>(req_n[r]),
+                                                                   s.hpw == 2 ? q5 : q4, max_chunk);
                 const uint32_t nchunks = p > 0 ? (p + chunk - 1) / chunk : 1u;
                 req_chunk[r] = static_cast<int32_t>(chunk);
                 req_nchunks[r] = static_cast<int32_t>(nchunks);
