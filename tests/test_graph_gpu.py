@@ -2,7 +2,8 @@
 
 * tv_tree_attention_plan_device writes the host planner's items and merge groups,
   item for item, for the benchmark batches, ragged batches (trees of up to 2048 nodes
-  among them; 160 requests, past the cost-class ranking's 128) and forced chunk lengths.
+  among them; 100, 128, 140 and 160 requests for each form of the device planner) and
+  forced chunk lengths.
 * GraphedTreeAttention (device plan, capacity grids, no allocation) equals
   packed_tree_attention bit for bit.
 * PackedVerifyGraph: one capture, then replays with new prefix lengths, page tables,
@@ -13,6 +14,7 @@
 from __future__ import annotations
 
 import ctypes
+from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -82,15 +84,34 @@ def batches():
                                   [int(x) for x in rng.choice([1, 16, 32, 64], size=160)])
 
 
+def plan_inputs(seed, requests, choices, max_prefix):
+    """Just what the planners read (prefix lengths and node counts, host and device)."""
+    rng = np.random.default_rng(seed)
+    prefixes = [int(x) for x in rng.integers(0, max_prefix, size=requests)]
+    counts = [int(x) for x in rng.choice(choices, size=requests)]
+    return SimpleNamespace(prefix_lengths=prefixes, node_counts_host=counts, num_requests=requests, block_size=256,
+                           prefix_lens=torch.tensor(prefixes, dtype=torch.int32, device=DEV),
+                           node_counts=torch.tensor(counts, dtype=torch.int32, device=DEV))
+
+
 def shard_batches():
     """(name, metadata, KV heads): one- and two-head shards, where the planner refits its
-    chunk target to fill whole rounds of work items."""
+    chunk target to fill whole rounds of work items, and batches for each of the device
+    planner's forms: above 64 requests the per-request steps use the whole block (and the
+    refit its 5-way search), 128 requests fill the cost-class ranking, and above it the
+    items' keys are sorted, with unaligned (65-node) and aligned (512-node) multi-block
+    trees."""
     yield "cfg4/kv1", workloads.config4(DEV, kv_heads=1, requests=64).metadata, 1
     yield "cfg5/kv2", workloads.config5(DEV, kv_heads=2).metadata, 2
     rng = np.random.default_rng(8)
     prefixes = [int(x) for x in rng.integers(0, 30000, size=34)]
     counts = [int(x) for x in rng.choice([16, 32, 64], size=34)]
     yield "ragged34", ragged_metadata(3, prefixes, counts, pool_pages=8192), 8
+    yield "r100", plan_inputs(7, 100, [1, 16, 32, 64], 30000), 8
+    yield "r100/kv1", plan_inputs(11, 100, [16, 32, 64], 20000), 1
+    yield "r128", plan_inputs(12, 128, [16, 32], 30000), 8
+    yield "r140/unaligned", plan_inputs(9, 140, [1, 16, 65, 512], 2000), 8
+    yield "r140/aligned", plan_inputs(10, 140, [16, 512], 2000), 4
 
 
 @pytest.mark.parametrize("chunk_keys", [0, 64, 256])
