@@ -7,16 +7,19 @@
 // are launched with a capacity grid and their surplus workgroups exit on the counts
 // this planner writes.
 //
-// One 1024-thread workgroup:
+// One 1024-thread workgroup (steps 1 and 2 in wave 0 alone, one request per lane and no
+// barrier, for batches of at most 64 requests):
 //   1. per request: KV heads per group, node blocks, cost; the total cost (reduction);
 //   2. per request: prefix chunk length and count (the host formulas), item / group /
-//      slot counts, and their exclusive prefix sums (one scan);
+//      slot counts, and their exclusive prefix sums (one scan); the host's refit of the
+//      chunk target when the last round of items is part-empty;
 //   3. the items in the host comparator's order, (~cost, request, head group, chunk,
 //      block), longest first: up to 128 requests by ranking each request's two cost
 //      classes (its chunks before the last, its last chunk) and placing every item at its
 //      class's offset; larger batches by a bitonic sort of 64-bit keys in LDS;
 //   4. the XCD placement of the host (64-item windows, multi-block groups first,
-//      column-major), then the items and groups are written out.
+//      column-major), then the items and groups are written out; the cost-class path
+//      writes the items of plans whose placement needs no window ranking directly.
 // Capacity overflow writes zero counts and an error flag instead of writing past the
 // caller's arrays.
 #include <math.h>
@@ -207,7 +210,8 @@ __device__ __forceinline__ uint32_t chunk_of(uint32_t p, uint32_t n, int64_t q, 
 __global__ void __launch_bounds__(kPlanThreads)
 plan_device_kernel(const PlanArgs a) {
     __shared__ uint64_t keys[kMaxSortItems];
-    __shared__ __align__(16) int32_t stream_id[kMaxSortItems];   // (request, head group, chunk) of each sorted item
+    // The cost classes of step 3, then per sorted position the data of step 4's placement.
+    __shared__ __align__(16) int32_t stream_id[kMaxSortItems];
     __shared__ int32_t req_p[kMaxPlanRequests], req_n[kMaxPlanRequests];
     __shared__ int32_t req_chunk[kMaxPlanRequests], req_nchunks[kMaxPlanRequests];
     __shared__ int32_t req_item_off[kMaxPlanRequests], req_group_off[kMaxPlanRequests], req_slot_off[kMaxPlanRequests];
