@@ -314,9 +314,10 @@ int tv_tree_attention_plan_slots(const int32_t* prefix_lens_host, const int32_t*
  * equivalent of target_graph.py:95-167 reading live metadata).  No counterpart kernel
  * in the reference: its Triton kernels read prefix lengths in every program.
  * tv_tree_attention_plan_capacity gives capacities that hold for any prefix length up
- * to max_prefix with these node counts (items <= CUs + sum of node-block groups x
- * (1 + chunks forced by the LDS page cache), or groups x ceil(max_prefix / chunk_keys)
- * for a forced chunk length), and the workspace those need.
+ * to max_prefix with these node counts (items <= the smaller of 2 x CUs + sum of
+ * node-block groups x (1 + chunks forced by the LDS page cache) and groups x
+ * ceil(max_prefix / 64), or groups x ceil(max_prefix / chunk_keys) for a forced chunk
+ * length), and the workspace those need.
  * tv_tree_attention_plan_device writes items [item_capacity, 8], groups
  * [group_capacity, 8] and counts[4] = {items, groups, partial slots, error}; on overflow
  * it writes zero counts and error 1 instead of overrunning the arrays.

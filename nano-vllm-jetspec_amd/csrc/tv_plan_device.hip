@@ -880,14 +880,18 @@ namespace {
 // items <= 2 * CUs + blocks * (1 + ceil(P_max / longest chunk)).  A chunk is at least
 // total/CUs keys per unit of cost unless it is capped by the LDS page cache, and the
 // round-filling refit keeps the item count within the rounds that count needed, so it
-// adds at most CUs - 1 items.  A forced chunk length gives every node-block group
-// ceil(P_max / chunk) items.
+// adds at most CUs - 1 items.  The chunk count is also ceil(p / c0) with c0 >= 64 keys,
+// so items <= blocks * ceil(P_max / 64) as well, which is the smaller bound for short
+// prefixes (every surplus workgroup of a capacity grid still takes a CU's LDS for a
+// moment).  A forced chunk length gives every node-block group ceil(P_max / chunk) items.
 int fill_capacity(int64_t blocks, int32_t max_nodes, int32_t block_size, int32_t num_compute_units,
                   int32_t chunk_keys, int64_t max_prefix, tv_attention_plan_info* info) {
     const int64_t max_chunk = (static_cast<int64_t>(kMaxChunkPages - 1) * block_size) / 32 * 32;
     const int64_t capped = (max_prefix + max_chunk - 1) / max_chunk;
+    const int64_t shortest = blocks * std::max<int64_t>(1, (max_prefix + kMinChunkKeys - 1) / kMinChunkKeys);
     const int64_t items = chunk_keys > 0 ? blocks * std::max<int64_t>(1, (max_prefix + chunk_keys - 1) / chunk_keys)
-                                         : 2 * static_cast<int64_t>(num_compute_units) + blocks * (1 + capped);
+                                         : std::min(2 * static_cast<int64_t>(num_compute_units) + blocks * (1 + capped),
+                                                    shortest);
     if (items > kMaxSortItems) {
         return fail(TV_ERR_UNSUPPORTED, "plan_capacity: %lld items exceed the device planner's %d",
                     static_cast<long long>(items), kMaxSortItems);
