@@ -57,12 +57,6 @@ struct PlanArgs {
 // Nodes of one KV head per work item and the two-head rule of the host planner (tv_plan.cpp).
 __host__ __device__ __forceinline__ int nodes_per_item(int hpw, int qpk) { return (8 / hpw) * (32 / qpk); }
 
-__device__ __forceinline__ int heads_per_group(int nodes, int kv_heads, int qpk) {
-    int h = nodes <= nodes_per_item(2, qpk) ? 2 : 1;
-    while (h > 1 && h > kv_heads) h >>= 1;
-    return h;
-}
-
 __device__ __forceinline__ int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 // Cost of one key of a work item in quarter key-steps of a one-head item: a two-head
@@ -153,8 +147,8 @@ __device__ int64_t block_sum(int64_t v, int waves, int64_t* scratch) {
 }
 
 // One request's geometry from its (clamped) node count: KV heads per item, nodes per item,
-// head groups and node blocks (heads_per_group and nodes_per_item with nw = 32 / qpk nodes
-// per wave taken once per thread, so only the node-block count divides).
+// head groups and node blocks (the host planner's heads_per_group and nodes_per_item, with
+// nw = 32 / qpk nodes per wave taken once per thread, so only the node-block count divides).
 struct ReqShape {
     int hpw, npw, G, NB;
 };
