@@ -33,7 +33,7 @@ namespace tv {
 namespace {
 
 constexpr int kPlanThreads = 1024;
-constexpr int kMaxSortItems = 8192;      // LDS sort capacity (64 KiB of keys)
+constexpr int kMaxSortItems = 8192;      // items of one plan (64 KiB of sorted keys in LDS)
 constexpr int kMaxPlanRequests = 2048;
 // A sorted position holds (request in bits 32-47, enumeration index in bits 0-31); the
 // XCD placement may park a 16-bit position in bits 48-63.

@@ -123,7 +123,7 @@ def test_device_plan_equals_host_plan(chunk_keys):
                          queries_per_kv=4)
         print(f"[plan] {name} chunk={chunk_keys} items={host['num_items']} groups={host['num_groups']}", flush=True)
         if host["num_items"] > 8192:
-            # Beyond the device planner's LDS sort: refused up front, never overrun.
+            # Beyond the device planner's 8192 items (its LDS arrays): refused up front, never overrun.
             with pytest.raises(ValueError, match="exceed"):
                 device_plan(meta, kv_heads=kv, chunk_keys=chunk_keys)
             continue
