@@ -472,6 +472,34 @@ def test_plan_fills_its_rounds_of_work_items():
     assert plan["num_items"] == 1152 and plan["num_groups"] == 0
 
 
+def test_split_prefix_last_chunk_ends_level_with_the_others():
+    """The last chunk of a split prefix also walks the tree (two prefix keys' worth per node).
+    Within the chunk count the prefix alone gives, the chunks are cut so that the last one,
+    with its tree, is at most a 32-key step longer than the others, unless lengthening the
+    others by that step would leave the last chunk no prefix keys (the count would change)."""
+    rng = np.random.default_rng(12)
+    checked = 0
+    for _ in range(200):
+        count = int(rng.integers(1, 12))
+        prefixes = [int(x) for x in rng.integers(0, 6000, size=count)]
+        nodes = [int(x) for x in rng.choice([1, 16, 32, 64, 100, 512], size=count)]
+        plan = make_plan(prefixes, nodes, 8, 256, 256, queries_per_kv=4)
+        for r, (p, t) in enumerate(zip(prefixes, nodes)):
+            items = plan["items"][(plan["items"][:, 0] == r) & (plan["items"][:, 1] == 0) & (plan["items"][:, 2] == 0)]
+            if len(items) < 2:
+                continue
+            lengths = sorted({int(e - b) for b, e, f in zip(items[:, 3], items[:, 4], items[:, 5]) if not f & 1})
+            last = [int(e - b) for b, e, f in zip(items[:, 3], items[:, 4], items[:, 5]) if f & 1]
+            assert len(lengths) == 1 and len(last) == 1, (p, t)
+            chunk, nc = lengths[0], len(items)
+            assert chunk % 32 == 0 and 1 <= last[0] <= chunk and (nc - 1) * chunk + last[0] == p
+            # Equal chunks alone would give ceil(p / nc) rounded up to 32; the tree moves keys off the last.
+            assert chunk >= (p + nc - 1) // nc
+            assert last[0] + 2 * t <= chunk + 32 or (nc - 1) * (chunk + 32) >= p, (p, t, chunk, last)
+            checked += 1
+    assert checked > 100
+
+
 def _capacity(lib, counts, kv_heads, block, cus, chunk, max_prefix, groups=4):
     info = _lib.PlanInfo()
     arr = (ctypes.c_int32 * len(counts))(*counts)
