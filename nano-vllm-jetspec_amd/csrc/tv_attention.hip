@@ -104,50 +104,60 @@ merge_partials_kernel(const AttnParams p) {
     for (int group = blockIdx.x; group < count; group += gridDim.x) merge_group<T>(p, group);
 }
 
-// One thread per (row, word) of the ancestor bits.  Row i of a tree of tn nodes carries bits
-// for its elements m <= i; the word's elements that do (lim of them) are loaded without
-// conditions, every load clamped into that range so that all 64 issue back to back, then
-// masked.  Elements past the node or past the tree are not read; any element at or before
-// the node that is neither 0 nor -inf sets TV_STATUS_BAD_BIAS.
-constexpr int kPackThreads = 256;
+// One wave per row of the ancestor bits.  Row i of a tree of tn nodes carries bits for its
+// elements m <= i; word w is the ballot of the zeros among elements 64w..64w+63, which the
+// wave's lanes read with one coalesced 256-byte load (indices clamped into the row's first
+// i + 1 elements, so nothing past the node is read).  A wave issues the loads of up to
+// kPackBatch words before their ballots and writes every word of its row, zeros past the
+// node.  Any element at or before the node that is neither 0 nor -inf sets
+// TV_STATUS_BAD_BIAS.  (One wave per word made as many waves as words, each waiting out its
+// own chain of dependent loads; one thread per word read 64 scattered rows per load.)
+constexpr int kPackWaves = 4;   // rows per 256-thread workgroup
+constexpr int kPackBatch = 8;   // words whose loads a wave issues together
 
-__global__ void __launch_bounds__(kPackThreads)
+__global__ void __launch_bounds__(64 * kPackWaves)
 pack_ancestor_kernel(const float* __restrict__ bias, const int64_t* __restrict__ bias_off,
                      const int32_t* __restrict__ q2r, const int32_t* __restrict__ local,
                      const int32_t* __restrict__ counts, int32_t total_q, int32_t num_requests, int32_t words,
                      uint64_t* __restrict__ out, int32_t* status) {
-    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (idx >= static_cast<int64_t>(total_q) * words) return;
-    const int64_t q = idx / words;
-    const int w = static_cast<int>(idx - q * words);
+    const int lane = threadIdx.x & 63;
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * kPackWaves + (threadIdx.x >> 6);   // wave-uniform
+    if (q >= total_q) return;
     const int r = q2r[q];
-    uint64_t word = 0;
+    int lim = 0;   // elements of the row that carry bits
+    const float* row = bias;
     if (r < 0 || r >= num_requests) {
-        set_status(status, TV_STATUS_BAD_REQUEST);
+        if (lane == 0) set_status(status, TV_STATUS_BAD_REQUEST);
     } else {
         const int i = local[q];
         const int tn = counts[r];
         if (i >= 0 && i < tn) {
-            const int lim = min(tn, i + 1) - 64 * w;   // elements of this word that carry bits
-            if (lim > 0) {
-                const float* seg = bias + bias_off[r] + static_cast<int64_t>(i) * tn + 64 * w;
-                float x[64];
-#pragma unroll
-                for (int b = 0; b < 64; ++b) x[b] = seg[min(b, lim - 1)];
-                bool other = false;   // a value bits cannot carry
-#pragma unroll
-                for (int b = 0; b < 64; ++b) {
-                    const bool in = b < lim;
-                    word |= static_cast<uint64_t>(in && x[b] == 0.f) << b;
-                    other |= in && x[b] != 0.f && x[b] != -INFINITY;
-                }
-                if (other) set_status(status, TV_STATUS_BAD_BIAS);
-            }
-        } else {
+            lim = i + 1;
+            row = bias + bias_off[r] + static_cast<int64_t>(i) * tn;
+        } else if (lane == 0) {
             set_status(status, TV_STATUS_BAD_REQUEST);
         }
     }
-    out[idx] = word;
+    const int used = (lim + 63) / 64;   // words with an element that carries a bit
+    uint64_t* row_out = out + q * words;
+    bool other = false;   // a value bits cannot carry
+    for (int w0 = 0; w0 < words; w0 += kPackBatch) {
+        float x[kPackBatch];
+#pragma unroll
+        for (int k = 0; k < kPackBatch; ++k) {
+            x[k] = w0 + k < used ? row[min(64 * (w0 + k) + lane, lim - 1)] : -INFINITY;
+        }
+        uint64_t mine = 0;   // lane k keeps word w0 + k
+#pragma unroll
+        for (int k = 0; k < kPackBatch; ++k) {
+            const bool in = 64 * (w0 + k) + lane < lim;
+            const uint64_t bits = __ballot(in && x[k] == 0.f);
+            other |= in && x[k] != 0.f && x[k] != -INFINITY;
+            if (lane == k) mine = bits;
+        }
+        if (lane < kPackBatch && w0 + lane < words) row_out[w0 + lane] = mine;
+    }
+    if (__ballot(other) && lane == 0) set_status(status, TV_STATUS_BAD_BIAS);
 }
 
 }  // namespace
@@ -167,9 +177,8 @@ extern "C" int tv_pack_ancestor_words(const float* qq_bias, const int64_t* qq_bi
     if (!qq_bias || !qq_bias_offsets || !query_to_request || !query_local_row || !node_counts || !words) {
         return fail(TV_ERR_INVALID, "pack_ancestor_words: null pointer");
     }
-    const int64_t n = static_cast<int64_t>(total_queries) * words_per_row;
-    const int64_t blocks = (n + kPackThreads - 1) / kPackThreads;
-    hipLaunchKernelGGL(pack_ancestor_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kPackThreads), 0,
+    const int64_t blocks = (static_cast<int64_t>(total_queries) + kPackWaves - 1) / kPackWaves;
+    hipLaunchKernelGGL(pack_ancestor_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(64 * kPackWaves), 0,
                        as_stream(stream), qq_bias,
                        qq_bias_offsets, query_to_request, query_local_row, node_counts, total_queries,
                        num_requests, words_per_row, words, status);
