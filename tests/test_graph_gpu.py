@@ -139,6 +139,51 @@ def test_device_plan_equals_host_plan(chunk_keys):
         assert np.array_equal(groups[:host["num_groups"]], host["groups"][:host["num_groups"]]), name
 
 
+def test_device_plan_equals_host_plan_on_random_batches():
+    """Seeded random batches over every form of the device planner: request counts on both
+    sides of its one-wave (64), cost-class (128) and sort limits, one to eight KV heads,
+    1 to 16 query heads per KV head, trees of 1 to 2048 nodes (aligned and unaligned
+    multi-block ones), prefixes from empty to 200k keys, pages of 32 and 256 and forced
+    chunk lengths.  Batches whose plan either planner refuses (capacity) are counted, not
+    compared; most are compared."""
+    rng = np.random.default_rng(2024)
+    cus = _device.compute_units(torch.cuda.current_device())
+    compared = refused = 0
+    for trial in range(240):
+        requests = int(rng.choice([1, 2, 3, 7, 8, 16, 33, 63, 64, 65, 100, 127, 128, 129, 200, 300]))
+        kv = int(rng.choice([1, 2, 4, 8]))
+        qpk = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16]))
+        kind = trial % 4
+        if kind == 0:
+            counts = rng.integers(1, 65, size=requests)
+        elif kind == 1:
+            counts = rng.choice([1, 16, 32, 64, 65, 100, 512, 1024], size=requests)
+        elif kind == 2:
+            counts = rng.choice([8, 512], size=requests)
+        else:
+            counts = rng.integers(1, 2049, size=requests)
+        prefixes = rng.integers(0, int(rng.choice([1, 100, 3000, 30000, 200000])), size=requests)
+        chunk = int(rng.choice([0, 0, 0, 64, 256]))
+        block = int(rng.choice([32, 256]))
+        meta = SimpleNamespace(prefix_lengths=[int(x) for x in prefixes], node_counts_host=[int(x) for x in counts],
+                               num_requests=requests, block_size=block,
+                               prefix_lens=torch.tensor(prefixes, dtype=torch.int32, device=DEV),
+                               node_counts=torch.tensor(counts, dtype=torch.int32, device=DEV))
+        case = f"trial {trial}: R={requests} kv={kv} G={qpk} kind={kind} chunk={chunk} page={block}"
+        try:
+            host = make_plan(meta.prefix_lengths, meta.node_counts_host, kv, block, cus, chunk, queries_per_kv=qpk)
+            items, groups, got, _ = device_plan(meta, kv_heads=kv, chunk_keys=chunk, queries_per_kv=qpk)
+        except ValueError:
+            refused += 1
+            continue
+        compared += 1
+        assert got == [host["num_items"], host["num_groups"], host["num_partial_slots"], 0], case
+        assert np.array_equal(items[:host["num_items"]], host["items"]), case
+        assert np.array_equal(groups[:host["num_groups"]], host["groups"][:host["num_groups"]]), case
+    print(f"[plan fuzz] compared {compared}, refused {refused}", flush=True)
+    assert compared >= 150
+
+
 def test_capacity_overflow_writes_zero_counts():
     meta = ragged_metadata(3, [100000], [64])
     lib = _lib.library()
