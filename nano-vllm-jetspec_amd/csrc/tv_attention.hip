@@ -22,7 +22,10 @@ namespace {
 template <typename T>
 __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     const int32_t* gr = p.groups + 8 * static_cast<int64_t>(group);
-    const int r = gr[0], h0 = gr[1], n0 = gr[2], hpw = gr[3], first = gr[4], ns = gr[5];
+    // The group record is the same for the whole workgroup: scalar registers.
+    const int r = __builtin_amdgcn_readfirstlane(gr[0]), h0 = __builtin_amdgcn_readfirstlane(gr[1]);
+    const int n0 = __builtin_amdgcn_readfirstlane(gr[2]), hpw = __builtin_amdgcn_readfirstlane(gr[3]);
+    const int first = __builtin_amdgcn_readfirstlane(gr[4]), ns = __builtin_amdgcn_readfirstlane(gr[5]);
     if (r < 0 || r >= p.num_requests || h0 < 0 || n0 < 0 || (hpw != 1 && hpw != 2) || first < 0 || ns < 1 ||
         first > p.num_slots - ns || gr[6] != p.qpk) {
         if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
@@ -41,19 +44,29 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     // stay in bounds and the row is dropped at the end), 8 partials at a time, with the
     // running maximum rescaled between batches.  Up to 8 partials this is the plain
     // maximum-then-sum.
-    const float2* ml = p.ws_ml + static_cast<int64_t>(first) * kRowsPerItem + wr;
-    // Partial rows are D floats apart.  A thread merges dims 4*quad..4*quad+3 and, at head
-    // size 256, the same 128 dims further; quads past D / 4 (head size 64) have none.
+    // Partial s of this thread's row sits at the group's base plus s partial strides plus
+    // the row's own offset: the bases are wave-uniform (scalar registers) and the row
+    // offsets 32-bit, so the addresses of the 8 partials in flight cost few vector
+    // registers.  With a 64-bit vector address per partial the merge took 125 registers,
+    // 4 waves per SIMD (config 2: 10.1 us); this form takes 79 and 6 waves (9.1 us).
     const int D = p.head_dim;
-    const float* prow = p.ws_o + (static_cast<int64_t>(first) * kRowsPerItem + wr) * D;
-    const int tn = p.cnt[r], qbase = p.cu[r];
+    const uint64_t ml_step = static_cast<uint64_t>(kRowsPerItem) * sizeof(float2);
+    const uint64_t o_step = static_cast<uint64_t>(kRowsPerItem) * D * sizeof(float);
+    const char* ml_base = reinterpret_cast<const char*>(p.ws_ml) + static_cast<uint64_t>(first) * ml_step;
+    const char* o_base = reinterpret_cast<const char*>(p.ws_o) + static_cast<uint64_t>(first) * o_step;
+    const uint32_t ml_off = static_cast<uint32_t>(wr) * sizeof(float2);
+    const uint32_t o_row = static_cast<uint32_t>(wr * D) * sizeof(float);
+    const int tn = __builtin_amdgcn_readfirstlane(p.cnt[r]), qbase = __builtin_amdgcn_readfirstlane(p.cu[r]);
     if (qbase < 0 || tn < 0 || tn > p.total_queries - qbase) {   // rows outside the packed batch
         if (blockIdx.y == 0 && threadIdx.x == 0) set_status(p.status, TV_STATUS_BAD_REQUEST);
         return;
     }
     const bool row_ok = head < p.num_kv_heads && node < tn && c < nw * G;   // c >= nw * G: padding row
+    // Partial rows are D floats apart.  A thread merges dims 4*quad..4*quad+3 and, at head
+    // size 256, the same 128 dims further; quads past D / 4 (head size 64) have none.
+#pragma unroll 1
     for (int d4 = 4 * quad; d4 < D; d4 += 128) {
-        const float* po = prow + d4;
+        const uint32_t po_off = o_row + static_cast<uint32_t>(d4) * sizeof(float);
         float m = -INFINITY, l = 0.f;
         f32x4 o = {0.f, 0.f, 0.f, 0.f};
         for (int s0 = 0; s0 < ns; s0 += 8) {
@@ -62,8 +75,9 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 if (s0 + k < ns) {
-                    part[k] = ml[static_cast<int64_t>(s0 + k) * kRowsPerItem];
-                    po4[k] = *reinterpret_cast<const f32x4*>(po + static_cast<int64_t>(s0 + k) * kRowsPerItem * D);
+                    const uint64_t s = static_cast<uint64_t>(s0 + k);
+                    part[k] = *reinterpret_cast<const float2*>(ml_base + s * ml_step + ml_off);
+                    po4[k] = *reinterpret_cast<const f32x4*>(o_base + s * o_step + po_off);
                 } else {
                     part[k] = make_float2(-INFINITY, 0.f);
                     po4[k] = f32x4{0.f, 0.f, 0.f, 0.f};

@@ -597,8 +597,9 @@ def _legacy_mfma(q, k_pool, v_pool, req, scale, num_queries_per_kv: int, block_s
         prefixes_host, nodes_host, 1, num_kv_heads, num_queries_per_kv, cus, 0,
         items.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), groups.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
         ctypes.byref(info)), "tree_attention_plan_slots")
-    items_dev = torch.from_numpy(items).to(device)
-    groups_dev = torch.from_numpy(groups).to(device)
+    # Pinned and asynchronous, as the packed path's plan: no wait on the stream's queued work.
+    staged = _device.upload_fields({"items": items, "groups": groups}, device, pinned=True)
+    items_dev, groups_dev = staged["items"], staged["groups"]
     ws_bytes = workspace_bytes(info.workspace_bytes, info.num_partial_slots, int(q.shape[2]))
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
