@@ -39,11 +39,8 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
     const int head = h0 + hl;
     const int node = n0 + nw * (wave - hl * wph) + c / G;
     const int qh = head * G + c % G;
-    // Every partial of the group and the request's row offset are loaded together (a
-    // row past the tree or past the last head has slots too, never written; its loads
-    // stay in bounds and the row is dropped at the end), 8 partials at a time, with the
-    // running maximum rescaled between batches.  Up to 8 partials this is the plain
-    // maximum-then-sum.
+    // Every partial of a row is loaded together, 8 partials at a time, with the running
+    // maximum rescaled between batches.  Up to 8 partials this is the plain maximum-then-sum.
     // Partial s of this thread's row sits at the group's base plus s partial strides plus
     // the row's own offset: the bases are wave-uniform (scalar registers) and the row
     // offsets 32-bit, so the addresses of the 8 partials in flight cost few vector
@@ -62,6 +59,9 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
         return;
     }
     const bool row_ok = head < p.num_kv_heads && node < tn && c < nw * G;   // c >= nw * G: padding row
+    // Rows past the tree (or padding) were never written and are not stored: no loads.  A
+    // 16-node tree leaves 3 of every 4 rows of its 64-node block empty.
+    if (!row_ok) return;
     // Partial rows are D floats apart.  A thread merges dims 4*quad..4*quad+3 and, at head
     // size 256, the same 128 dims further; quads past D / 4 (head size 64) have none.
 #pragma unroll 1
@@ -102,7 +102,7 @@ __device__ __forceinline__ void merge_group(const AttnParams& p, int group) {
             }
             m = mb;
         }
-        if (row_ok) store_out4<T>(p, qbase + node, qh, d4, o * (1.f / l));
+        store_out4<T>(p, qbase + node, qh, d4, o * (1.f / l));
     }
 }
 
